@@ -1,0 +1,193 @@
+"""Benchmark of the int4 KV-cache attention path on one MI355X.
+
+A step is one split-KV decode + log-sum-exp merge of 2 query tokens (MTP 1) over a 131072-token int4 paged cache,
+24 query / 4 KV heads, head 256, block 16, 8192 shuffled blocks (workload decode-int4-128k-t2): one attention layer
+of one decode step. Inputs are seeded synthetic data resident in HBM before timing.
+
+Prints one JSON line: decode tok/s (value), HBM GB/s and us per layer, the prefill-chunk workload's tok/s when the
+prefill kernel is available, the roofline of the decode kernel (algorithmic bytes / its average duration measured with
+events on its stream) and the CPU baseline (the dequantise-then-attend restatement timed on this host).
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--segments N] [--no-cpu] [--no-prefill]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "vllm-quantpack_amd"))
+
+METRIC = "int4-KV decode tok/s + HBM GB/s at 128k ctx; prefill-chunk tok/s"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def decode_bench(torch, args):
+    from vllm_quantpack.attention import int4_kv
+    from vllm_quantpack.tools import synth
+    dev = torch.device("cuda:0")
+    w = synth.make("decode-int4-128k-t2")
+    d = synth.to_device(w, dev)
+    S = args.segments or int4_kv.segments_for(torch.cuda.get_device_properties(0).multi_processor_count)
+    T, NQ, HS = w.q.shape
+    so = torch.empty((T, NQ, S, HS), dtype=torch.float32, device=dev)
+    sm = torch.empty((T, NQ, S), dtype=torch.float32, device=dev)
+    ss = torch.empty((T, NQ, S), dtype=torch.float32, device=dev)
+    out = torch.empty((T, NQ, HS), dtype=torch.bfloat16, device=dev)
+    plan = int4_kv.DecodePlan(d["q"], d["k_cache"], d["v_cache"], d["k_scale_cache"], d["v_scale_cache"], out,
+                              cu_seqlens_q=d["cu_seqlens_q"], seqused_k=d["seqused_k"],
+                              block_table=d["block_table"], max_seqlen_q=w.max_query_len,
+                              softmax_scale=w.softmax_scale, num_segments=S, softmax_segm_output=so,
+                              softmax_segm_max=sm, softmax_segm_expsum=ss)
+    for _ in range(args.warmup):
+        plan.run()
+    torch.cuda.synchronize()
+    # timed region: exactly `steps` steps; decode-kernel events on the launch stream
+    stream = torch.cuda.current_stream(dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for a, b in ev:
+        a.record(stream)
+        plan.decode()
+        b.record(stream)
+        plan.merge()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    kern_ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
+    step_ms = elapsed * 1e3 / args.steps
+    nbytes = synth.cache_bytes(w)
+    result = dict(tokens_per_step=T, step_ms=step_ms, decode_kernel_us=kern_ms * 1e3, bytes=nbytes, segments=S,
+                  out=out, w=w)
+    return result
+
+
+def prefill_bench(torch, args):
+    from vllm_quantpack.attention import int4_kv, int4_prefill
+    from vllm_quantpack.tools import synth
+    dev = torch.device("cuda:0")
+    w = synth.make("prefill-int4-128k-c1024")
+    d = synth.to_device(w, dev)
+    out = torch.empty_like(d["q"])
+
+    def step():
+        int4_kv.reshape_and_cache_int4  # noqa: B018  (store is timed separately below)
+        int4_prefill.prefill_attention(d["q"], d["k_cache"], d["v_cache"], d["k_scale_cache"], d["v_scale_cache"],
+                                       out, cu_seqlens_q=d["cu_seqlens_q"], seqused_k=d["seqused_k"],
+                                       block_table=d["block_table"], max_seqlen_q=w.max_query_len,
+                                       softmax_scale=w.softmax_scale)
+
+    from vllm_quantpack.attention import k8v4_kv
+    k8v4_kv.store(None, d["new_key"], d["new_value"], d["k_cache"], d["v_cache"], d["new_slots"],
+                  k_scale_cache=d["k_scale_cache"], v_scale_cache=d["v_scale_cache"], rotate=False)
+    step()
+    torch.cuda.synchronize()
+    reps = 5
+    stream = torch.cuda.current_stream(dev)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(reps):
+        step()
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    chunk = w.q.shape[0]
+    n = int(w.seqused_k[0])
+    cached = n - chunk
+    flops = 4.0 * w.head_size * w.num_q_heads * (chunk * cached + chunk * (chunk + 1) / 2)
+    return dict(ms=ms, tok_s=chunk / (ms * 1e-3), tflops=flops / (ms * 1e-3) / 1e12, flops=flops)
+
+
+def cpu_baseline(w, budget_s=20.0):
+    """The oracle's dequantise-then-attend restatement of the reference's path, on this host's cores."""
+    import numpy as np
+    import torch
+
+    from oracle import qp_oracle as O
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    views = O.int4_views(w.kv, w.head_size)
+    q = O.bf16_bits_to_f32(w.q)
+    n = int(w.seqused_k[0])
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 and (not times or time.perf_counter() - t_start + times[-1] < budget_s):
+        t = time.perf_counter()
+        O.prefill_dequant_attend(q, views, w.block_table[0], n, w.softmax_scale)
+        times.append(time.perf_counter() - t)
+    med = float(np.median(times))
+    return dict(value=round(q.shape[0] / med, 3), unit="tok/s", cores=threads, kind="port",
+                sample=f"full decode-int4-128k-t2 step ({q.shape[0]} query tokens over {n} keys), median of "
+                       f"{len(times)} reps, {med:.2f} s each, torch {torch.__version__} CPU")
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--segments", type=int, default=0, help="split-KV segments (default: sized for the CU count)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-chunk workload")
+    args = ap.parse_args(argv)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X: the int4 KV attention path has no multi-GPU step in this build "
+              "(it shards by KV head with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    log(f"device {torch.cuda.get_device_name(0)}, {torch.cuda.get_device_properties(0).multi_processor_count} CUs")
+    r = decode_bench(torch, args)
+    step_s = r["step_ms"] * 1e-3
+    kern_s = r["decode_kernel_us"] * 1e-6
+    log(f"decode: {r['step_ms'] * 1e3:.1f} us/step, decode kernel {r['decode_kernel_us']:.1f} us, "
+        f"{r['bytes'] / kern_s / 1e9:.0f} GB/s")
+    line = {
+        "metric": METRIC,
+        "value": round(r["tokens_per_step"] / step_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["step_ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "decode-int4-128k-t2", "context": 131072, "query_tokens": 2, "q_heads": 24,
+                   "kv_heads": 4, "head_size": 256, "block_size": 16, "kv_format": "int4_per_token_head",
+                   "segments": r["segments"], "parallelism": "single-gpu"},
+        "us_per_layer": round(r["step_ms"] * 1e3, 2),
+        "hbm_gbps_step": round(r["bytes"] / step_s / 1e9, 1),
+        "hbm_gbps_decode_kernel": round(r["bytes"] / kern_s / 1e9, 1),
+        "roofline": {"bound": "hbm", "achieved": round(r["bytes"] / kern_s / 1e9, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(r["bytes"] / kern_s / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "qp::decode_kernel<256,0,1>",
+                     "bytes_per_launch": r["bytes"], "avg_us": round(r["decode_kernel_us"], 2)},
+    }
+    if not args.no_prefill:
+        try:
+            p = prefill_bench(torch, args)
+            line["prefill"] = {"workload": "prefill-int4-128k-c1024", "tok_s": round(p["tok_s"], 1),
+                               "ms": round(p["ms"], 3), "tflops": round(p["tflops"], 1),
+                               "mfma_frac": round(p["tflops"] / BF16_PEAK_TFLOPS, 4)}
+        except NotImplementedError as e:
+            line["prefill"] = {"workload": "prefill-int4-128k-c1024", "tok_s": None, "note": str(e)}
+    if not args.no_cpu:
+        log("CPU baseline ...")
+        line["cpu_baseline"] = cpu_baseline(r["w"])
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

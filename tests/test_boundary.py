@@ -1,0 +1,219 @@
+"""The drop-in boundary on the CPU: the C-ABI library exports what include/quantpack.h declares, the Python layer keeps
+the reference's names, known answers and error behaviour (tests/test_int4_kv.py:13-87, tests/test_k8v4_kv.py:16-51).
+No kernel runs here."""
+import ctypes
+import logging
+import os
+import re
+import sys
+import types
+
+import pytest
+import torch
+
+from conftest import REPO
+
+LOG = logging.getLogger("test")
+HEADER = os.path.join(REPO, "include", "quantpack.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(qp_\w+)\s*\(", src, flags=re.M)))
+
+
+def test_header_declares_the_entry_points():
+    assert _declared() == sorted(["qp_unpack_segment", "qp_decode_splitkv", "qp_merge_segments", "qp_prefill",
+                                  "qp_store", "qp_rht", "qp_last_error", "qp_version"])
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    from vllm_quantpack import _hip
+    if not os.path.exists(_hip.LIB_PATH):
+        pytest.skip("library not built (python vllm-quantpack_amd/build.py)")
+    lib = ctypes.CDLL(_hip.LIB_PATH)
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert set(_declared()) == set(_hip.SIGNATURES)
+    assert _hip.lib().qp_version().decode().startswith("quantpack-hip")
+
+
+def test_argument_errors_are_reported_without_a_gpu():
+    """Validation runs on the host before any launch: a bad call returns QP_ERR_INVALID with a message."""
+    from vllm_quantpack import _hip
+    if not os.path.exists(_hip.LIB_PATH):
+        pytest.skip("library not built")
+    cache = _hip.PagedCache()
+    args = _hip.DecodeArgs()
+    st = _hip.lib().qp_decode_splitkv(cache, args, None)
+    assert st == _hip.QP_ERR_INVALID
+    assert "null" in _hip.lib().qp_last_error().decode()
+    with pytest.raises(ValueError):
+        _hip.check(st, "decode")
+
+
+def test_missing_library_fails_loudly(monkeypatch):
+    from vllm_quantpack import _hip
+    monkeypatch.setattr(_hip, "_lib", None)
+    monkeypatch.setattr(_hip, "LIB_PATH", "/nonexistent/libquantpack_hip.so")
+    with pytest.raises(_hip.HipLibraryMissing):
+        _hip.lib()
+
+
+# --------------------------------------------------------------------------------- reference known answers
+
+def test_disabled_by_environment(monkeypatch):
+    from vllm_quantpack.attention import int4_kv
+    monkeypatch.setenv("VLLM_QUANTPACK_INT4_KV", "0")
+    assert int4_kv.patch_int4_kv(LOG) is False
+
+
+def test_vllm_without_int4_mode_leaves_everything(monkeypatch):
+    from vllm_quantpack.attention import int4_kv
+    monkeypatch.setattr(int4_kv, "MODULE", "vllm_quantpack_no_such_module")
+    assert int4_kv.patch_int4_kv(LOG) is False
+
+
+def _fake_triton_attn(monkeypatch):
+    mod = types.ModuleType("vllm.v1.attention.backends.triton_attn")
+    mod.NUM_PAR_SOFTMAX_SEGMENTS = 16
+
+    class Builder:
+        def __init__(self, kv_cache_spec, layer_names, vllm_config, device):
+            self.num_par_softmax_segments = mod.NUM_PAR_SOFTMAX_SEGMENTS
+
+    mod.TritonAttentionMetadataBuilder = Builder
+    for name in ("vllm", "vllm.v1", "vllm.v1.attention", "vllm.v1.attention.backends"):
+        monkeypatch.setitem(sys.modules, name, sys.modules.get(name) or types.ModuleType(name))
+    monkeypatch.setitem(sys.modules, mod.__name__, mod)
+    monkeypatch.setattr(sys.modules["vllm.v1.attention.backends"], "triton_attn", mod, raising=False)
+    return mod
+
+
+def _config(dtype):
+    return types.SimpleNamespace(cache_config=types.SimpleNamespace(cache_dtype=dtype))
+
+
+def test_decode_segments_only_for_int4_caches(monkeypatch):
+    from vllm_quantpack.attention import int4_kv
+    mod = _fake_triton_attn(monkeypatch)
+    assert int4_kv._patch_decode_segments(64, LOG) == 64
+    assert mod.TritonAttentionMetadataBuilder(None, [], _config("int4_per_token_head"), None).num_par_softmax_segments == 64
+    assert mod.TritonAttentionMetadataBuilder(None, [], _config("k8v4_per_token_head"), None).num_par_softmax_segments == 64
+    assert mod.TritonAttentionMetadataBuilder(None, [], _config("auto"), None).num_par_softmax_segments == 16
+    assert mod.NUM_PAR_SOFTMAX_SEGMENTS == 16
+
+
+def test_decode_segments_not_power_of_two_left_stock(monkeypatch):
+    from vllm_quantpack.attention import int4_kv
+    mod = _fake_triton_attn(monkeypatch)
+    assert int4_kv._patch_decode_segments(48, LOG) == 0
+    assert mod.TritonAttentionMetadataBuilder(None, [], _config("int4_per_token_head"), None).num_par_softmax_segments == 16
+
+
+def test_patch_installs_hip_functions_into_the_stock_module(monkeypatch):
+    """With a stand-in of vLLM's int4 module, patch_int4_kv rebinds unified_attention_int4 and the store."""
+    from vllm_quantpack import _hip
+    from vllm_quantpack.attention import int4_kv
+    if not os.path.exists(_hip.LIB_PATH):
+        pytest.skip("library not built")
+    stock = types.ModuleType("vllm_quantpack_fake_int4")
+    stock.unified_attention_int4 = lambda *a, **k: "stock"
+    stock.reshape_and_cache_int4 = lambda *a, **k: "stock"
+    monkeypatch.setitem(sys.modules, stock.__name__, stock)
+    monkeypatch.setattr(int4_kv, "MODULE", stock.__name__)
+    assert int4_kv.patch_int4_kv(LOG) is True
+    assert getattr(stock.unified_attention_int4, "_quantpack", False)
+    assert getattr(stock.reshape_and_cache_int4, "_quantpack", False)
+    assert int4_kv.patch_int4_kv(LOG) is True          # idempotent
+
+
+def test_decode_override_from_environment(monkeypatch):
+    from vllm_quantpack.attention import int4_kv
+    monkeypatch.setenv("VLLM_QUANTPACK_INT4_DECODE", "32,8,32")
+    assert int4_kv.decode_tiles(188) == (32, 8, 32)
+    monkeypatch.setenv("VLLM_QUANTPACK_INT4_DECODE", "64,4,auto")
+    assert int4_kv.decode_tiles(84) == (64, 4, 32)
+
+
+def test_decode_override_accepts_query_row_cap(monkeypatch):
+    from vllm_quantpack.attention import int4_kv
+    monkeypatch.setenv("VLLM_QUANTPACK_INT4_DECODE", "64,4,auto,16")
+    assert int4_kv.decode_tiles(188) == (64, 4, 64, 16)
+    monkeypatch.setenv("VLLM_QUANTPACK_INT4_DECODE", "64,4,32,32")
+    assert int4_kv.decode_tiles(84) == (64, 4, 32, 32)
+
+
+@pytest.mark.parametrize("sms,segments", [(188, 64), (84, 32), (36, 16), (8, 16), (132, 64), (512, 128), (256, 64)],
+                         ids=["rtx-pro-6000", "a40", "rtx-5060-ti", "tiny", "h100", "cap", "mi355x"])
+def test_segments_follow_cu_count(monkeypatch, sms, segments):
+    from vllm_quantpack.attention import int4_kv
+    monkeypatch.delenv("VLLM_QUANTPACK_INT4_DECODE", raising=False)
+    assert int4_kv.decode_tiles(sms) == (64, 4, segments)
+
+
+def test_cell_is_key_bytes_plus_packed_value_plus_two_scales():
+    from vllm_quantpack.attention import k8v4_kv
+    assert k8v4_kv.cell_bytes(256, 256) == 392
+    assert k8v4_kv.cell_bytes(128, 64) == 168
+
+
+@pytest.mark.parametrize("layout", ["hnd", "nhd"])
+def test_views_cover_the_cell_without_overlap(layout):
+    from vllm_quantpack.attention import k8v4_kv
+    nb, nkv, bs, hs = 3, 2, 4, 16
+    cell = k8v4_kv.cell_bytes(hs, hs)
+    if layout == "hnd":
+        kv = torch.zeros((nb, nkv, bs, cell), dtype=torch.int8)
+    else:
+        kv = torch.zeros((nb, bs, nkv, cell), dtype=torch.int8).transpose(1, 2)
+    key, value, ks, vs = k8v4_kv.views(kv, hs)
+    assert key.shape == (nb, bs, nkv, hs) and key.dtype == torch.int8
+    assert value.shape == (nb, bs, nkv, hs // 2) and value.dtype == torch.uint8
+    assert ks.shape == vs.shape == (nb, bs, nkv) and ks.dtype == torch.float32
+    key.fill_(1)
+    ks.view(torch.int32).fill_(0x02020202)
+    value.fill_(3)
+    vs.view(torch.int32).fill_(0x04040404)
+    want = torch.tensor([1] * hs + [2] * 4 + [3] * (hs // 2) + [4] * 4, dtype=torch.int8)
+    assert (kv == want).all()
+    ks[1, 2, 1] = 7.0
+    assert kv[1, 1, 2, hs:hs + 4].view(torch.float32).item() == 7.0
+
+
+def test_views_reject_another_cell_size():
+    from vllm_quantpack.attention import k8v4_kv
+    with pytest.raises(ValueError, match="expected 392"):
+        k8v4_kv.views(torch.zeros((1, 4, 16, 264), dtype=torch.int8), 256)
+
+
+def test_int4_cache_views_are_not_taken_for_k8v4():
+    from vllm_quantpack.attention import k8v4_kv
+    assert not k8v4_kv.is_k8v4(torch.zeros(1, dtype=torch.uint8))
+    assert k8v4_kv.is_k8v4(torch.zeros(1, dtype=torch.int8))
+
+
+def test_int4_views_match_the_reference_test_layout():
+    """tests/test_int4_kv.py:95-103: kc/vc (blocks, bs, nkv, hs/2 + 4) uint8 slices, fp32 scales at hs/2 and at
+    hs + 4 + hs/2 within each cell."""
+    from vllm_quantpack.attention import k8v4_kv
+    nb, nkv, bs, hs = 2, 4, 16, 256
+    kv = torch.zeros((nb, nkv, bs, hs + 8), dtype=torch.uint8)
+    kc, vc, ks, vs = k8v4_kv.int4_views(kv, hs)
+    assert kc.shape == vc.shape == (nb, bs, nkv, hs // 2 + 4)
+    assert kc.stride() == (nkv * bs * (hs + 8), hs + 8, bs * (hs + 8), 1)
+    ks[1, 3, 2] = 5.0
+    vs[1, 3, 2] = 6.0
+    assert kv[1, 2, 3, hs // 2:hs // 2 + 4].view(torch.float32).item() == 5.0
+    assert kv[1, 2, 3, hs + 4:hs + 8].view(torch.float32).item() == 6.0
+    assert vc.storage_offset() == hs // 2 + 4
+
+
+def test_unsupported_features_raise():
+    from vllm_quantpack.attention import int4_kv
+    q = torch.zeros((1, 24, 256), dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError, match="sliding window"):
+        int4_kv._plain(q, (128, 0), 0.0, None, None, None, None, None)
+    with pytest.raises(NotImplementedError, match="softcap"):
+        int4_kv._plain(q, (-1, -1), 30.0, None, None, None, None, None)

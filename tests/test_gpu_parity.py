@@ -1,0 +1,258 @@
+"""Parity of the HIP kernels with the CPU oracle, on seeded inputs (runs on the MI355X through the C ABI).
+
+Bars: the unpack and the store are bit-exact; attention is within 1e-2 relative (Frobenius, the reference's own test
+metric, tests/test_int4_kv.py:160-161,190) of the oracle's emulation of the reference's exact kernel, and within
+0.5 % of the fp64 closed form.
+"""
+import numpy as np
+import pytest
+
+from oracle import qp_oracle as O
+from qp_testlib import bf16_tensor, i32, random_cache, run_decode, to_f32, torch_cache
+
+pytestmark = pytest.mark.gpu
+
+NQ, NKV, HS = 24, 4, 256
+
+
+# ---------------------------------------------------------------------------------------------------- unpack
+
+@pytest.mark.parametrize("fmt,which", [("int4", "key"), ("int4", "value"), ("int8", "key")])
+@pytest.mark.parametrize("layout", ["hnd", "nhd"])
+@pytest.mark.parametrize("bs", [16, 3072])
+def test_unpack_segment_bit_exact(device, fmt, which, layout, bs):
+    import torch
+
+    from vllm_quantpack.attention import int4_prefill
+    rng = np.random.default_rng(hash((fmt, which, layout, bs)) % 2**32)
+    nb = 40 if bs == 16 else 3
+    kv, v = random_cache(rng, nb, NKV, bs, HS, fmt, layout)
+    _, (kc, vc, ks, vs) = torch_cache(kv, HS, fmt, device)
+    row = rng.permutation(nb).astype(np.int32)
+    start, length = (37, 500) if bs == 16 else (1000, 4500)
+    out = torch.full((length + 3, NKV, HS), float("nan"), dtype=torch.bfloat16, device=device)
+    cache, scales = (kc, ks) if which == "key" else (vc, vs)
+    int4_prefill.unpack_segment(cache, scales, i32(row, device), start, length, out)
+    torch.cuda.synchronize()
+    got = out[:length].view(torch.int16).cpu().numpy().view(np.uint16)
+    want = O.unpack_segment(v, row, start, length, which)
+    assert (got == want).all()
+    assert torch.isnan(out[length:].float()).all()        # nothing written past `length`
+
+
+# ---------------------------------------------------------------------------------------------------- decode
+
+def _decode_case(device, rng, fmt, lens, layout="hnd", bs=16, segments=8, nq=NQ, nkv=NKV, hs=HS, scale=None):
+    """lens = [(T_i, n_i)]: one call over the batch; returns (gpu out, oracle emulation, fp64 refs)."""
+    nbs = [-(-n // bs) for _, n in lens]
+    total = sum(nbs) + 3
+    kv, v = random_cache(rng, total, nkv, bs, hs, fmt, layout)
+    _, views = torch_cache(kv, hs, fmt, device)
+    pool = rng.permutation(total).astype(np.int32)
+    width = max(nbs)
+    table = np.zeros((len(lens), width), np.int32)
+    at = 0
+    for i, nb in enumerate(nbs):
+        table[i, :nb] = pool[at:at + nb]
+        at += nb
+    Ts = [t for t, _ in lens]
+    q = O.f32_to_bf16_bits(rng.standard_normal((sum(Ts), nq, hs)).astype(np.float32))
+    cu = np.concatenate(([0], np.cumsum(Ts))).astype(np.int32)
+    used = np.array([n for _, n in lens], np.int32)
+    scale = scale or hs ** -0.5
+    out, bufs = run_decode(views, bf16_tensor(q, device), i32(cu, device), i32(used, device), i32(table, device),
+                           max(Ts), scale, segments, device)
+    qf = O.bf16_bits_to_f32(q)
+    emus, refs = [], []
+    for i, (T, n) in enumerate(lens):
+        qs = qf[cu[i]:cu[i + 1]]
+        emus.append(O.decode_emulated(qs, v, table[i], n, scale, num_segments=segments, tile=32))
+        K, V = O.dequant_f64(v, table[i], n)
+        refs.append(O.attention_f64(qs, K, V, n, scale))
+    return out, np.concatenate(emus), np.concatenate(refs), dict(bufs=bufs, views=v, table=table, q=qf)
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+@pytest.mark.parametrize("T", [1, 2, 3, 4])
+def test_decode_matches_oracle(device, fmt, T):
+    rng = np.random.default_rng(100 + T + (10 if fmt == "int8" else 0))
+    out, emu, ref, _ = _decode_case(device, rng, fmt, [(T, 5003)], segments=7)
+    assert O.relerr(out, emu) < 1e-2
+    assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
+
+
+@pytest.mark.parametrize("layout,bs", [("nhd", 16), ("hnd", 32), ("hnd", 3072), ("nhd", 48)])
+def test_decode_layouts_and_block_sizes(device, layout, bs):
+    rng = np.random.default_rng(7 + bs)
+    out, emu, ref, _ = _decode_case(device, rng, "int4", [(2, 4100)], layout=layout, bs=bs, segments=5)
+    assert O.relerr(out, emu) < 1e-2
+    assert O.relerr(out, ref) < 5e-3
+
+
+def test_decode_ragged_batch(device):
+    """Sequences of 4, 3, 1 and 2 query tokens and very different lengths in one call (tests/test_int4_kv.py:230-249
+    with k8v4 keys, as the ragged k8v4 workload)."""
+    rng = np.random.default_rng(21)
+    lens = [(4, 2000), (3, 900), (1, 3333), (2, 64), (1, 1)]
+    out, emu, ref, _ = _decode_case(device, rng, "int8", lens, segments=16)
+    at = 0
+    for T, n in lens:
+        sl = slice(at, at + T)
+        assert O.relerr(out[sl], emu[sl]) < 1e-2, (T, n)
+        assert O.relerr(out[sl], ref[sl]) < 5e-3, (T, n)
+        at += T
+
+
+def test_decode_segment_count_invariance(device):
+    rng = np.random.default_rng(31)
+    outs = []
+    for S in (1, 4, 64, 200):
+        out, _, ref, _ = _decode_case(device, np.random.default_rng(31), "int4", [(2, 6000)], segments=S)
+        outs.append(out)
+        assert O.relerr(out, ref) < 5e-3, S
+    for o in outs[1:]:
+        assert O.relerr(o, outs[0]) < 3e-3
+
+
+def test_decode_partials_match_the_emulation(device):
+    """Per-segment (acc, m, l) against the emulation run with the kernel's 32-key segmentation."""
+    rng = np.random.default_rng(41)
+    T, n, S = 2, 3000, 6
+    out, emu, ref, ctx = _decode_case(device, rng, "int4", [(T, n)], segments=S)
+    so, sm, ss = ctx["bufs"]
+    acc, m, l_ = O.decode_partials(ctx["q"], ctx["views"], ctx["table"][0], n, HS ** -0.5, S, tile=32)
+    active = -(-n // O.segment_length(n, S, 32))
+    gm, gl, go = to_f32(sm)[:, :, :active], to_f32(ss)[:, :, :active], to_f32(so)[:, :, :active]
+    assert np.isfinite(gm).all() and np.isfinite(gl).all() and np.isfinite(go).all()
+    # the kernel may keep a different (lazily updated) reference maximum: compare rescaled to the oracle's
+    f = np.exp2(gm - m[:, :, :active])
+    assert np.allclose(gl * f, l_[:, :, :active], rtol=1e-3)
+    assert O.relerr(go * f[..., None], acc[:, :, :active]) < 1e-2
+
+
+def test_decode_gqa_8_and_head_128(device):
+    rng = np.random.default_rng(51)
+    out, emu, ref, _ = _decode_case(device, rng, "int4", [(4, 2500), (1, 700)], nq=16, nkv=2, hs=128, segments=9)
+    assert O.relerr(out, emu) < 1e-2
+    assert O.relerr(out, ref) < 5e-3
+
+
+# ------------------------------------------------------------------------------------------------------ store
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+@pytest.mark.parametrize("layout", ["hnd", "nhd"])
+def test_store_bit_exact(device, fmt, layout):
+    import torch
+
+    from vllm_quantpack.attention import k8v4_kv
+    rng = np.random.default_rng(61)
+    nb, bs, n = 20, 16, 200
+    kv_np = O.new_cache(nb, NKV, bs, O.int4_cell_bytes(HS) if fmt == "int4" else O.k8v4_cell_bytes(HS), layout)
+    t, (kc, vc, ks, vs) = torch_cache(kv_np, HS, fmt, device)
+    key = O.f32_to_bf16_bits(rng.standard_normal((n, NKV, HS)).astype(np.float32) * 2)
+    val = O.f32_to_bf16_bits(rng.standard_normal((n, NKV, HS)).astype(np.float32))
+    slots = rng.permutation(nb * bs)[:n].astype(np.int64)
+    slots[::17] = -1
+    k8v4_kv.store(None, bf16_tensor(key, device), bf16_tensor(val, device), kc, vc,
+                  torch.from_numpy(slots).to(device), k_scale_cache=ks, v_scale_cache=vs, rotate=False)
+    torch.cuda.synchronize()
+    views = O.int4_views(kv_np, HS) if fmt == "int4" else O.k8v4_views(kv_np, HS)
+    O.store(views, O.bf16_bits_to_f32(key), O.bf16_bits_to_f32(val), slots)
+    got = t.cpu().numpy().view(np.uint8)            # logical (blocks, heads, slots, cell) order
+    assert (got == kv_np).all()
+
+
+def test_store_with_rotation_equals_rotate_then_store(device):
+    import torch
+
+    from vllm_quantpack.attention import k8v4_kv, rht
+    rng = np.random.default_rng(62)
+    nb, bs, n = 10, 16, 150
+    kv_a = O.new_cache(nb, NKV, bs, O.k8v4_cell_bytes(HS))
+    kv_b = O.new_cache(nb, NKV, bs, O.k8v4_cell_bytes(HS))
+    ta, va = torch_cache(kv_a, HS, "int8", device)
+    tb, vb = torch_cache(kv_b, HS, "int8", device)
+    key = bf16_tensor(O.f32_to_bf16_bits(rng.standard_normal((n, NKV, HS)).astype(np.float32)), device)
+    val = bf16_tensor(O.f32_to_bf16_bits(rng.standard_normal((n, NKV, HS)).astype(np.float32)), device)
+    slots = torch.arange(n, device=device)
+    k8v4_kv.store(None, key, val, va[0], va[1], slots, k_scale_cache=va[2], v_scale_cache=va[3])
+    k8v4_kv.store(None, rht.single_rht(key), rht.single_rht(val), vb[0], vb[1], slots, k_scale_cache=vb[2],
+                  v_scale_cache=vb[3], rotate=False)
+    torch.cuda.synchronize()
+    assert torch.equal(ta, tb)
+
+
+# -------------------------------------------------------------------------------------------------------- RHT
+
+def test_rht_matches_fp64_and_inverts(device):
+    import torch
+
+    from vllm_quantpack.attention import rht
+    rng = np.random.default_rng(71)
+    x = rng.standard_normal((33, HS)).astype(np.float32)
+    xt = torch.from_numpy(x).to(device)
+    y = rht.single_rht(xt)
+    want = O.rht(x)
+    assert np.allclose(to_f32(y), want, rtol=1e-5, atol=1e-4)
+    back = rht.single_rht(y, inverse=True, out_scale=1.0 / HS)
+    assert np.allclose(to_f32(back), x, atol=1e-5)
+    yb = rht.single_rht(xt.to(torch.bfloat16))
+    assert (to_f32(yb) == O.round_bf16(O.rht(O.round_bf16(x)).astype(np.float32))).mean() > 0.99
+
+
+# --------------------------------------------------------------------------------- end-to-end drop-in router
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+@pytest.mark.parametrize("qlen", [1, 2, 4])
+def test_unified_attention_decode_matches_fp64(device, fmt, qlen):
+    """The reference's end-to-end check (tests/test_int4_kv.py:172-191 / test_k8v4_kv.py:506-520): random bf16 K/V
+    stored through reshape_and_cache_int4, attention of unrotated queries against fp64, error < 1e-2 (and < 0.5 %)."""
+    import torch
+
+    from vllm_quantpack.attention import int4_kv
+    rng = np.random.default_rng(81 + qlen)
+    n, bs = 6000, 16
+    nb = -(-n // bs)
+    kv_np = O.new_cache(nb, NKV, bs, O.int4_cell_bytes(HS) if fmt == "int4" else O.k8v4_cell_bytes(HS))
+    _, (kc, vc, ks, vs) = torch_cache(kv_np, HS, fmt, device)
+    g = torch.Generator(device=device).manual_seed(0)
+    k = torch.randn((n, NKV, HS), generator=g, device=device, dtype=torch.bfloat16)
+    v = torch.randn((n, NKV, HS), generator=g, device=device, dtype=torch.bfloat16)
+    int4_kv.reshape_and_cache_int4(k, v, kc, vc, torch.arange(n, device=device), k_scale_cache=ks,
+                                   v_scale_cache=vs)
+    q = torch.randn((qlen, NQ, HS), generator=g, device=device, dtype=torch.bfloat16)
+    S = 64
+    rows = 32
+    segm = (torch.empty((rows, NQ, S, HS), dtype=torch.float32, device=device),
+            torch.empty((rows, NQ, S), dtype=torch.float32, device=device),
+            torch.empty((rows, NQ, S), dtype=torch.float32, device=device))
+    out = torch.empty_like(q)
+    int4_kv.unified_attention_int4(
+        q, kc, vc, out, cu_seqlens_q=i32([0, qlen], device), max_seqlen_q=qlen, seqused_k=i32([n], device),
+        max_seqlen_k=n, softmax_scale=HS ** -0.5, window_size=(-1, -1),
+        block_table=torch.arange(nb, dtype=torch.int32, device=device)[None], softcap=0.0, sinks=None,
+        alibi_slopes=None, use_alibi_sqrt=False, qq_bias=None, output_scale=None, mm_prefix_range=None,
+        k_scale_cache=ks, v_scale_cache=vs, seq_threshold_3D=rows, num_par_softmax_segments=S,
+        softmax_segm_output=segm[0], softmax_segm_max=segm[1], softmax_segm_expsum=segm[2])
+    torch.cuda.synchronize()
+    # fp64 reference from the stored bytes (the cache is in the rotated domain)
+    views = O.int4_views if fmt == "int4" else O.k8v4_views
+    root = _host_cache(kc, vc, ks, vs, fmt)
+    K, V = O.dequant_f64(views(root, HS), np.arange(nb), n)
+    qr = O.rht(to_f32(q).astype(np.float64))
+    ref = O.rht(O.attention_f64(qr, K, V, n, HS ** -0.5 / HS), inverse=True) / HS
+    err = O.relerr(to_f32(out), ref)
+    assert err < 5e-3, err
+
+
+def _host_cache(kc, vc, ks, vs, fmt):
+    """The byte cache behind the views, copied to the host as a numpy (blocks, heads, slots, cell) array."""
+    import torch
+    st = kc.untyped_storage()
+    nbytes = st.nbytes()
+    base = torch.empty(nbytes, dtype=torch.uint8, device=kc.device)
+    base.set_(st, 0, (nbytes,), (1,))
+    arr = base.cpu().numpy()
+    nb, bs, nkv = kc.shape[0], kc.shape[1], kc.shape[2]
+    cell = O.int4_cell_bytes(HS) if fmt == "int4" else O.k8v4_cell_bytes(HS)
+    return arr.reshape(nb, nkv, bs, cell)

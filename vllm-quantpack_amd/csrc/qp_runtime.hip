@@ -1,0 +1,29 @@
+// Host-side error channel and version of libquantpack_hip.so.
+#include "qp_common.h"
+
+namespace qp {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string &msg) { g_last_error = msg; }
+
+int fail(int code, const std::string &msg) {
+  g_last_error = msg;
+  return code;
+}
+
+// Status of the launch just issued on this thread: 0 or the hipError_t it raised.
+int launch_status() {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    g_last_error = std::string("kernel launch failed: ") + hipGetErrorString(e);
+    return (int)e;
+  }
+  return QP_OK;
+}
+
+}  // namespace qp
+
+extern "C" const char *qp_last_error(void) { return qp::g_last_error.c_str(); }
+
+extern "C" const char *qp_version(void) { return "quantpack-hip 0.1.0 gfx950"; }
