@@ -110,8 +110,8 @@ def test_decode_segment_count_invariance(device):
         out, _, ref, _ = _decode_case(device, np.random.default_rng(31), "int4", [(2, 6000)], segments=S)
         outs.append(out)
         assert O.relerr(out, ref) < 5e-3, S
-    for o in outs[1:]:
-        assert O.relerr(o, outs[0]) < 3e-3
+    for o in outs[1:]:      # each is ~2e-3 from fp64 (bf16 P_v and output rounding): independent roundings
+        assert O.relerr(o, outs[0]) < 5e-3
 
 
 def test_decode_partials_match_the_emulation(device):

@@ -37,18 +37,13 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_
 
 // -------------------------------------------------------------------------------------- nibble unpack
 //
-// A bf16 with biased exponent 134 (0x43xx) covers [128, 256) in steps of 1, so OR-ing a nibble n into the low
-// mantissa bits gives exactly 128 + n. A nibble sitting at bits 4..7 lands in mantissa bits 4..7 under exponent
-// 138 (0x45xx): exactly 16 * (128 + n). Both are exact bf16 integers; callers fold the +128 into a zero-point term
-// and the x16 into the matching operand (a power of two, so that scaling is exact as well).
+// A bf16 with biased exponent 134 (0x43xx) covers [128, 256) in steps of 1: OR-ing a nibble n into mantissa bits
+// 0..3 gives exactly 128 + n. (Only bits 0..6 of a bf16 are mantissa, so a nibble must be moved down to bits 0..3
+// first; bit 7 already belongs to the exponent.) Callers fold the +128 into a zero-point term.
 //
-// From a dword x holding nibbles n0..n7 at bits 0,4,...,28 (two bytes per 16-bit half):
-//   lo_pair(x)        = (128 + n0, 128 + n4)
-//   hi_pair(x)        = 16 * (128 + n1, 128 + n5)
-//   lo_pair(x >> 8)   = (128 + n2, 128 + n6)
-//   hi_pair(x >> 8)   = 16 * (128 + n3, 128 + n7)
-__device__ __forceinline__ uint32_t nib_lo_pair(uint32_t x) { return (x & 0x000F000Fu) | 0x43004300u; }
-__device__ __forceinline__ uint32_t nib_hi_pair(uint32_t x) { return (x & 0x00F000F0u) | 0x45004500u; }
+// From a dword x holding nibbles n0..n7 at bits 0,4,...,28 (two bytes per 16-bit half), nib_pair(x >> 4c) is the
+// bf16 pair (128 + n_c, 128 + n_{c+4}), c = 0..3.
+__device__ __forceinline__ uint32_t nib_pair(uint32_t x) { return (x & 0x000F000Fu) | 0x43004300u; }
 
 // ---------------------------------------------------------------------------------------------- MFMA
 

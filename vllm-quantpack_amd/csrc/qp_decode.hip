@@ -13,9 +13,9 @@
 //   * Each wave streams its own 32-key chunks (chunk w, w+4, ...): codes go HBM -> VGPR (buffer loads whose per-key
 //     offsets live in SGPRs) -> wave-private LDS rows, prefetching the next chunk while the current one computes.
 //   * QK^T runs as S^T = K Q^T on v_mfma_f32_16x16x32_bf16 with the K tile as the A operand: nibbles become exact
-//     bf16 integers 128 + n (or 16 * (128 + n)) with two VALU ops per pair, and the Q operand is permuted and
-//     scaled to match. The S^T accumulator layout (4 keys x 1 query row per lane) is exactly the B operand layout of
-//     O^T = V^T P^T, so P never leaves registers.
+//     bf16 integers 128 + n (a shift and an and-or per pair), and the Q operand is permuted to match. The S^T
+//     accumulator layout (4 keys x 1 query row per lane) is exactly the B operand layout of O^T = V^T P^T, so P
+//     never leaves registers.
 //   * V is read from LDS as 16-bit pieces of two keys, giving per lane the per-channel key pairs the V^T A operand
 //     needs (the transpose costs no extra VALU).
 //   * The +128 offsets are removed through per-key scalars: S uses (128 + zp_k) * sum(q); the output subtracts
@@ -173,14 +173,14 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeParams p) {
     for (int mi = 0; mi < Sh::kNmi; ++mi) {
       u32x4_t x = rv ? *reinterpret_cast<const u32x4_t *>(qr + 8 * mi) : u32x4_t{0u, 0u, 0u, 0u};
       if constexpr (KFMT == QP_CODES_INT4) {
-        // K operand element order per 8 channels: (c0, c4, c1/16, c5/16, c2, c6, c3/16, c7/16), see nib_*_pair.
-        const float c1 = bf16_hi(x[0]), c3 = bf16_hi(x[1]), c5 = bf16_hi(x[2]), c7 = bf16_hi(x[3]);
-        qs += bf16_lo(x[0]) + c1 + bf16_lo(x[1]) + c3 + bf16_lo(x[2]) + c5 + bf16_lo(x[3]) + c7;
+        // K operand element order per 8 channels: (c0, c4, c1, c5, c2, c6, c3, c7), see nib_pair.
+        qs += bf16_lo(x[0]) + bf16_hi(x[0]) + bf16_lo(x[1]) + bf16_hi(x[1]) + bf16_lo(x[2]) + bf16_hi(x[2]) +
+              bf16_lo(x[3]) + bf16_hi(x[3]);
         u32x4_t y;
         y[0] = (x[0] & 0xFFFFu) | (x[2] << 16);
-        y[1] = pack_bf16x2(c1 * 0.0625f, c5 * 0.0625f);
+        y[1] = (x[0] >> 16) | (x[2] & 0xFFFF0000u);
         y[2] = (x[1] & 0xFFFFu) | (x[3] << 16);
-        y[3] = pack_bf16x2(c3 * 0.0625f, c7 * 0.0625f);
+        y[3] = (x[1] >> 16) | (x[3] & 0xFFFF0000u);
         qop[ct][mi] = as_bf16x8(y);
       } else {
         qop[ct][mi] = as_bf16x8(x);
@@ -270,8 +270,9 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeParams p) {
         }
 #pragma unroll
         for (int mi = 0; mi < Sh::kNmi; ++mi) {
-          const uint32_t x = kd[mi], y = x >> 8;
-          const bf16x8_t kop = as_bf16x8(u32x4_t{nib_lo_pair(x), nib_hi_pair(x), nib_lo_pair(y), nib_hi_pair(y)});
+          const uint32_t x = kd[mi];
+          const bf16x8_t kop =
+              as_bf16x8(u32x4_t{nib_pair(x), nib_pair(x >> 4), nib_pair(x >> 8), nib_pair(x >> 12)});
 #pragma unroll
           for (int ct = 0; ct < NCT; ++ct)
             sacc[ct][st] = mfma16x16x32(kop, qop[ct][mi], mi == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sacc[ct][st]);
@@ -373,10 +374,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeParams p) {
       for (int c = 0; c < 4; ++c) {
         u32x4_t vv;
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const uint32_t y = (c >= 2) ? (x[d] >> 8) : x[d];
-          vv[d] = (c & 1) ? nib_hi_pair(y) : nib_lo_pair(y);
-        }
+        for (int d = 0; d < 4; ++d) vv[d] = nib_pair(x[d] >> (4 * c));
         const bf16x8_t vop = as_bf16x8(vv);
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct)
@@ -428,9 +426,9 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeParams p) {
           for (int j = 0; j < 4; ++j) {
             float4 v;
             v.x = (acc[ct][b * 4 + 0][j] - cr) * fown[ct];
-            v.y = (acc[ct][b * 4 + 1][j] * 0.0625f - cr) * fown[ct];
+            v.y = (acc[ct][b * 4 + 1][j] - cr) * fown[ct];
             v.z = (acc[ct][b * 4 + 2][j] - cr) * fown[ct];
-            v.w = (acc[ct][b * 4 + 3][j] * 0.0625f - cr) * fown[ct];
+            v.w = (acc[ct][b * 4 + 3][j] - cr) * fown[ct];
             float4 *dst = reinterpret_cast<float4 *>(orow + 64 * b + 16 * g + 4 * j);
             if (ww == 0) {
               *dst = v;
