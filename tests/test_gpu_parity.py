@@ -89,6 +89,18 @@ def test_decode_layouts_and_block_sizes(device, layout, bs):
     assert O.relerr(out, ref) < 5e-3
 
 
+@pytest.mark.parametrize("fmt,T", [("int4", 1), ("int4", 2), ("int4", 4), ("int8", 2)])
+def test_decode_span_and_row_loaders_agree(device, fmt, T, monkeypatch):
+    """The HND page-span kernel (HBM -> LDS copies) and the generic strided-row kernel on the same cache."""
+    monkeypatch.delenv("QP_DECODE_ROWS", raising=False)
+    a, emu, ref, _ = _decode_case(device, np.random.default_rng(5), fmt, [(T, 3000), (1, 200)], segments=9)
+    monkeypatch.setenv("QP_DECODE_ROWS", "1")
+    b, _, _, _ = _decode_case(device, np.random.default_rng(5), fmt, [(T, 3000), (1, 200)], segments=9)
+    assert O.relerr(a, emu) < 1e-2 and O.relerr(b, emu) < 1e-2
+    assert O.relerr(a, ref) < 5e-3 and O.relerr(b, ref) < 5e-3
+    assert O.relerr(a, b) < 5e-3
+
+
 def test_decode_ragged_batch(device):
     """Sequences of 4, 3, 1 and 2 query tokens and very different lengths in one call (tests/test_int4_kv.py:230-249
     with k8v4 keys, as the ragged k8v4 workload)."""

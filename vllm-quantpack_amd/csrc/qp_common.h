@@ -43,7 +43,9 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_
 //
 // From a dword x holding nibbles n0..n7 at bits 0,4,...,28 (two bytes per 16-bit half), nib_pair(x >> 4c) is the
 // bf16 pair (128 + n_c, 128 + n_{c+4}), c = 0..3.
-__device__ __forceinline__ uint32_t nib_pair(uint32_t x) { return (x & 0x000F000Fu) | 0x43004300u; }
+__device__ __forceinline__ uint32_t nib_pair(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_bitop3_b32(x, 0x000F000Fu, 0x43004300u, 0xEA);  // (x & m) | c, one v_bitop3
+}
 
 // ---------------------------------------------------------------------------------------------- MFMA
 

@@ -7,21 +7,23 @@
 //   P_v16 = bf16(exp(S - m) * s_v),  acc += P_v16 . (v_codes - zp_v)  with the zero point taken on the same
 //   rounded P_v16 (int4_kv.py:90-94); l sums the unrounded exp(S - m).
 //
-// MI355X design (one workgroup = 4 waves per (segment, KV head, sequence)):
+// MI355X design (one workgroup of W waves per (segment, KV head, sequence)):
 //   * Every query row of the KV head's GQA group (T tokens x G heads, up to 32 rows) sits in one workgroup, so the
 //     segment's cache bytes are read from HBM once per step.
-//   * Each wave streams its own 32-key chunks (chunk w, w+4, ...): codes go HBM -> VGPR (buffer loads whose per-key
-//     offsets live in SGPRs) -> wave-private LDS rows, prefetching the next chunk while the current one computes.
+//   * Each wave streams its own 32-key chunks (chunk w, w + W, ...) into wave-private LDS. For the standard HND
+//     cache (each (block, KV head) page span of 16 cells contiguous) the span bytes go straight from HBM to LDS with
+//     global_load_lds_dwordx4 (no VGPR staging), double-buffered, waits placed by hand; any other strided layout
+//     goes through VGPR buffer loads into padded LDS rows.
 //   * QK^T runs as S^T = K Q^T on v_mfma_f32_16x16x32_bf16 with the K tile as the A operand: nibbles become exact
-//     bf16 integers 128 + n (a shift and an and-or per pair), and the Q operand is permuted to match. The S^T
+//     bf16 integers 128 + n (one v_bitop3 per pair plus shifts), the Q operand is permuted to match. The S^T
 //     accumulator layout (4 keys x 1 query row per lane) is exactly the B operand layout of O^T = V^T P^T, so P
 //     never leaves registers.
 //   * V is read from LDS as 16-bit pieces of two keys, giving per lane the per-channel key pairs the V^T A operand
-//     needs (the transpose costs no extra VALU).
+//     needs.
 //   * The +128 offsets are removed through per-key scalars: S uses (128 + zp_k) * sum(q); the output subtracts
 //     sum(P_v16 * (128 + zp_v)), accumulated from the same rounded P_v16 that feeds the MFMA.
-//   * Online softmax in base 2 with a lazy rescale (only when a row maximum grows); the 4 waves' states merge in
-//     LDS at the end and the workgroup writes one (acc, m, l) partial per row.
+//   * Online softmax in base 2 with a lazy rescale (only when a row maximum grows); the waves' states merge in LDS
+//     at the end and the workgroup writes one (acc, m, l) partial per row.
 #include "qp_common.h"
 
 namespace qp {
@@ -51,29 +53,337 @@ struct DecodeParams {
   float scale_log2;             // softmax_scale * log2(e)
 };
 
+constexpr int kChunk = QP_DECODE_TILE;  // keys per wave iteration: two 16-key sub-tiles
+
+__device__ __forceinline__ int fast_div(int x, uint32_t magic, uint32_t shift) {
+  return (int)(__umulhi((uint32_t)x, magic) >> shift);
+}
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// --------------------------------------------------------------------------------------- per-wave state
+
 template <int HS, int KFMT, int NCT>
-struct DecodeShape {
-  static constexpr int kWaves = 4;
-  static constexpr int kChunk = QP_DECODE_TILE;                   // keys per wave iteration (two 16-key sub-tiles)
+struct WaveState {
+  static constexpr int kNmi = HS / 32;  // QK MFMAs per 16-key sub-tile (32 channels each)
+  static constexpr int kNb = HS / 64;   // PV channel blocks (16 channel quads each)
+  bf16x8_t qop[NCT][kNmi];              // B operand of S^T = K Q^T
+  float qsum[NCT];                      // sum of the row's query channels (int4 zero-point term)
+  int row_pos[NCT];                     // absolute position of the row's query token
+  float m[NCT], l[NCT], c[NCT];         // running max (log2 units), sum of P, sum of P_v16 (128 + zp_v)
+  f32x4_t acc[NCT][kNb * 4];            // O^T tiles: tile (b, c) row j -> channel 64 b + 16 g + 4 j + c
+};
+
+template <int HS, int KFMT, int NCT>
+__device__ __forceinline__ void init_state(WaveState<HS, KFMT, NCT> &st, const DecodeParams &p, int q0, int T, int n,
+                                           int h, int G, int col, int g) {
+  const int R = T * G;
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    const int r = ct * 16 + col;
+    const bool rv = r < R;
+    const int t = (rv ? r : R - 1) / G, j = (rv ? r : R - 1) % G;
+    st.row_pos[ct] = n - T + t;
+    const uint16_t *qr = p.q + (int64_t)(q0 + t) * p.qs0 + (int64_t)(h * G + j) * p.qs1 + (HS / 4) * g;
+    float qs = 0.f;
+#pragma unroll
+    for (int mi = 0; mi < HS / 32; ++mi) {
+      const u32x4_t x = rv ? *reinterpret_cast<const u32x4_t *>(qr + 8 * mi) : u32x4_t{0u, 0u, 0u, 0u};
+      if constexpr (KFMT == QP_CODES_INT4) {
+        // K operand element order per 8 channels: (c0, c4, c1, c5, c2, c6, c3, c7), see nib_pair.
+        qs += bf16_lo(x[0]) + bf16_hi(x[0]) + bf16_lo(x[1]) + bf16_hi(x[1]) + bf16_lo(x[2]) + bf16_hi(x[2]) +
+              bf16_lo(x[3]) + bf16_hi(x[3]);
+        u32x4_t y;
+        y[0] = (x[0] & 0xFFFFu) | (x[2] << 16);
+        y[1] = (x[0] >> 16) | (x[2] & 0xFFFF0000u);
+        y[2] = (x[1] & 0xFFFFu) | (x[3] << 16);
+        y[3] = (x[1] >> 16) | (x[3] & 0xFFFF0000u);
+        st.qop[ct][mi] = as_bf16x8(y);
+      } else {
+        st.qop[ct][mi] = as_bf16x8(x);
+      }
+    }
+    if constexpr (KFMT == QP_CODES_INT4) {
+      qs += shfl_xor_f(qs, 16);
+      qs += shfl_xor_f(qs, 32);
+    }
+    st.qsum[ct] = qs;
+    st.m[ct] = -INFINITY;
+    st.l[ct] = 0.f;
+    st.c[ct] = 0.f;
+#pragma unroll
+    for (int i = 0; i < HS / 16; ++i) st.acc[ct][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+}
+
+// Per-key scalars of one key from its two words: (a_k, b_k) = (s_k * scale_log2, (128 + zp_k) * a_k) for the key
+// half, (s_v, 128 + zp_v) for the value half; zeros for keys at or past kend.
+template <int KFMT>
+__device__ __forceinline__ float2 key_floats(uint32_t word, bool is_value, bool ok, float scale_log2) {
+  if (!ok) return make_float2(0.f, 0.f);
+  if (is_value) return make_float2(__uint_as_float(word & 0xFFFFFFF0u), (float)(128u + (word & 0xFu)));
+  if constexpr (KFMT == QP_CODES_INT4) {
+    const float a = __uint_as_float(word & 0xFFFFFFF0u) * scale_log2;
+    return make_float2(a, a * (float)(128u + (word & 0xFu)));
+  } else {
+    return make_float2(__uint_as_float(word) * scale_log2, 0.f);
+  }
+}
+
+// ------------------------------------------------------------------------------------- one 32-key chunk
+//
+// kb/vb: LDS rows of the chunk's 32 keys (key kk at kb + kk * KSTR, vb + kk * VSTR); fb: float4 per key.
+template <int HS, int KFMT, int NCT, int KSTR, int VSTR>
+__device__ __forceinline__ void compute_chunk(WaveState<HS, KFMT, NCT> &st, const uint8_t *kb, const uint8_t *vb,
+                                              const uint8_t *fb, int k0, int kend, int causal_lim, int col, int g) {
+  constexpr int kKeyBytes = KFMT == QP_CODES_INT4 ? HS / 2 : HS;
+  constexpr int kNmi = HS / 32, kNb = HS / 64;
+
+  // ---- S^T = K Q^T, two 16-key sub-tiles
+  f32x4_t sacc[NCT][2];
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    const uint8_t *kr = kb + (sub * 16 + col) * KSTR + (kKeyBytes / 4) * g;
+    if constexpr (KFMT == QP_CODES_INT4) {
+      uint32_t kd[kNmi];
+#pragma unroll
+      for (int i = 0; i < kNmi; i += 2) {
+        const u32x2_t v2 = *reinterpret_cast<const u32x2_t *>(kr + 4 * i);
+        kd[i] = v2[0];
+        kd[i + 1] = v2[1];
+      }
+#pragma unroll
+      for (int mi = 0; mi < kNmi; ++mi) {
+        const uint32_t x = kd[mi], y = x >> 4;
+        const bf16x8_t kop = as_bf16x8(u32x4_t{nib_pair(x), nib_pair(y), nib_pair(x >> 8), nib_pair(y >> 8)});
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct)
+          sacc[ct][sub] = mfma16x16x32(kop, st.qop[ct][mi], mi == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sacc[ct][sub]);
+      }
+    } else {
+#pragma unroll
+      for (int mi = 0; mi < kNmi; ++mi) {
+        const u32x2_t x = *reinterpret_cast<const u32x2_t *>(kr + 8 * mi);
+        u32x4_t y;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint32_t src = x[d >> 1] >> (16 * (d & 1));
+          y[d] = pack_bf16x2((float)(int8_t)(src & 0xFF), (float)(int8_t)(src >> 8));
+        }
+        const bf16x8_t kop = as_bf16x8(y);
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct)
+          sacc[ct][sub] = mfma16x16x32(kop, st.qop[ct][mi], mi == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sacc[ct][sub]);
+      }
+    }
+  }
+
+  // ---- per-key scalars of the lane's 8 keys: 4g + j (sub-tile 0) and 16 + 4g + j (sub-tile 1)
+  float4 kf[2][4];
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) kf[sub][j] = *reinterpret_cast<const float4 *>(fb + (sub * 16 + 4 * g + j) * 16);
+
+  const bool need_mask = k0 + kChunk > causal_lim;
+  u32x4_t pop[NCT];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    float s[2][4];
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (KFMT == QP_CODES_INT4)
+          s[sub][j] = fmaf(sacc[ct][sub][j], kf[sub][j].x, -st.qsum[ct] * kf[sub][j].y);
+        else
+          s[sub][j] = sacc[ct][sub][j] * kf[sub][j].x;
+      }
+    if (need_mask) {
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int key = k0 + sub * 16 + 4 * g + j;
+          if (key > st.row_pos[ct] || key >= kend) s[sub][j] = -INFINITY;
+        }
+    }
+    float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                     fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+    mx = fmaxf(mx, shfl_xor_f(mx, 16));
+    mx = fmaxf(mx, shfl_xor_f(mx, 32));
+    if (__any(mx > st.m[ct])) {
+      const float m_new = fmaxf(st.m[ct], mx);
+      const float alpha = st.m[ct] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m[ct] - m_new);
+      st.l[ct] *= alpha;
+      st.c[ct] *= alpha;
+#pragma unroll
+      for (int i = 0; i < kNb * 4; ++i) st.acc[ct][i] *= alpha;
+      st.m[ct] = m_new;
+    }
+    const float mu = st.m[ct] == -INFINITY ? 0.f : st.m[ct];
+    float lsum = 0.f, csum = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const int sub = d >> 1, j0 = (d & 1) * 2;
+      const float p0 = __builtin_amdgcn_exp2f(s[sub][j0] - mu);
+      const float p1 = __builtin_amdgcn_exp2f(s[sub][j0 + 1] - mu);
+      lsum += p0 + p1;
+      const uint32_t pk = pack_bf16x2(p0 * kf[sub][j0].z, p1 * kf[sub][j0 + 1].z);
+      csum = fmaf(bf16_lo(pk), kf[sub][j0].w, csum);
+      csum = fmaf(bf16_hi(pk), kf[sub][j0 + 1].w, csum);
+      pop[ct][d] = pk;
+    }
+    st.l[ct] += lsum;
+    st.c[ct] += csum;
+  }
+
+  // ---- O^T += V^T P^T
+#pragma unroll
+  for (int b = 0; b < kNb; ++b) {
+    uint32_t x[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const int ka = (d < 2 ? 4 * g + 2 * d : 16 + 4 * g + 2 * (d - 2));
+      const uint8_t *vr = vb + 2 * (col + 16 * b);
+      const uint32_t lo = *reinterpret_cast<const uint16_t *>(vr + ka * VSTR);
+      const uint32_t hi = *reinterpret_cast<const uint16_t *>(vr + (ka + 1) * VSTR);
+      x[d] = lo | (hi << 16);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      u32x4_t vv;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) vv[d] = nib_pair(x[d] >> (4 * c));
+      const bf16x8_t vop = as_bf16x8(vv);
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+        st.acc[ct][b * 4 + c] = mfma16x16x32(vop, as_bf16x8(pop[ct]), st.acc[ct][b * 4 + c]);
+    }
+  }
+}
+
+// ------------------------------------------------------------------------ merge of the waves, partial out
+//
+// smem must hold 2 * WAVES * NCT * 16 floats of statistics plus NCT * 16 rows of (HS + 4) floats, and be free.
+template <int HS, int KFMT, int NCT, int WAVES>
+__device__ __forceinline__ void finish_workgroup(WaveState<HS, KFMT, NCT> &st, uint8_t *smem, const DecodeParams &p,
+                                                 int w, int col, int g, int q0, int T, int G, int h, int seg_idx) {
+  constexpr int kORow = HS + 4;
+  const int R = T * G;
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    st.l[ct] += shfl_xor_f(st.l[ct], 16);
+    st.l[ct] += shfl_xor_f(st.l[ct], 32);
+    st.c[ct] += shfl_xor_f(st.c[ct], 16);
+    st.c[ct] += shfl_xor_f(st.c[ct], 32);
+  }
+  __syncthreads();
+  float *st_m = reinterpret_cast<float *>(smem);
+  float *st_l = st_m + WAVES * NCT * 16;
+  float *obuf = st_l + WAVES * NCT * 16;
+  if (g == 0) {
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      st_m[(w * NCT + ct) * 16 + col] = st.m[ct];
+      st_l[(w * NCT + ct) * 16 + col] = st.l[ct];
+    }
+  }
+  __syncthreads();
+  float fown[NCT];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < WAVES; ++ww) M = fmaxf(M, st_m[(ww * NCT + ct) * 16 + col]);
+    fown[ct] = st.m[ct] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m[ct] - M);
+  }
+  for (int ww = 0; ww < WAVES; ++ww) {
+    if (w == ww) {
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        float *orow = obuf + (ct * 16 + col) * kORow;
+        const float cr = st.c[ct], f = fown[ct];
+#pragma unroll
+        for (int b = 0; b < HS / 64; ++b)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            float4 v;
+            v.x = (st.acc[ct][b * 4 + 0][j] - cr) * f;
+            v.y = (st.acc[ct][b * 4 + 1][j] - cr) * f;
+            v.z = (st.acc[ct][b * 4 + 2][j] - cr) * f;
+            v.w = (st.acc[ct][b * 4 + 3][j] - cr) * f;
+            float4 *dst = reinterpret_cast<float4 *>(orow + 64 * b + 16 * g + 4 * j);
+            if (ww == 0) {
+              *dst = v;
+            } else {
+              const float4 o = *dst;
+              *dst = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+            }
+          }
+      }
+    }
+    __syncthreads();
+  }
+  for (int idx = threadIdx.x; idx < R * (HS / 4); idx += WAVES * 64) {
+    const int r = idx / (HS / 4), c4 = idx % (HS / 4);
+    const int t = r / G, j = r % G;
+    float *dst = p.so + (int64_t)(q0 + t) * p.sos0 + (int64_t)(h * G + j) * p.sos1 + (int64_t)seg_idx * p.sos2;
+    reinterpret_cast<float4 *>(dst)[c4] = reinterpret_cast<const float4 *>(obuf + r * kORow)[c4];
+  }
+  if (w == 0 && g == 0) {
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      const int r = ct * 16 + col;
+      if (r < R) {
+        float M = -INFINITY, L = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < WAVES; ++ww) M = fmaxf(M, st_m[(ww * NCT + ct) * 16 + col]);
+#pragma unroll
+        for (int ww = 0; ww < WAVES; ++ww) {
+          const float mw = st_m[(ww * NCT + ct) * 16 + col];
+          if (mw != -INFINITY) L += st_l[(ww * NCT + ct) * 16 + col] * __builtin_amdgcn_exp2f(mw - M);
+        }
+        const int t = r / G, j = r % G;
+        const int64_t o = (int64_t)(q0 + t) * p.sts0 + (int64_t)(h * G + j) * p.sts1 + seg_idx;
+        p.smax[o] = M;
+        p.ssum[o] = L;
+      }
+    }
+  }
+}
+
+template <int HS, int NCT, int WAVES>
+constexpr int merge_lds_bytes() {
+  return 2 * WAVES * NCT * 16 * 4 + NCT * 16 * (HS + 4) * 4;
+}
+
+// --------------------------------------------------------------- generic strided layout: VGPR-staged loader
+
+template <int HS, int KFMT>
+struct RowShape {
   static constexpr int kKeyBytes = KFMT == QP_CODES_INT4 ? HS / 2 : HS;
   static constexpr int kValBytes = HS / 2;
-  static constexpr int kKRow = kKeyBytes + 16;                    // padded LDS rows: conflict-free b128 / u16 reads
+  static constexpr int kKRow = kKeyBytes + 16;  // padded LDS rows
   static constexpr int kVRow = kValBytes + 16;
-  static constexpr int kNmi = HS / 32;                            // QK MFMAs per sub-tile (32 channels each)
-  static constexpr int kNb = HS / 64;                             // PV channel blocks (16 channel quads each)
-  static constexpr int kKDw = kKeyBytes / 4;                      // dwords per key row
-  static constexpr int kVDw = kValBytes / 4;
-  static constexpr int kKpl = 64 / kKDw;                          // keys per wave load
-  static constexpr int kVpl = 64 / kVDw;
-  static constexpr int kKLoads = kChunk / kKpl;
-  static constexpr int kVLoads = kChunk / kVpl;
-  static constexpr int kKOff = 0;
+  static constexpr int kKDw = kKeyBytes / 4, kVDw = kValBytes / 4;
+  static constexpr int kKpl = 64 / kKDw, kVpl = 64 / kVDw;  // keys per wave load
+  static constexpr int kKLoads = kChunk / kKpl, kVLoads = kChunk / kVpl;
   static constexpr int kVOff = kChunk * kKRow;
-  static constexpr int kFOff = kVOff + kChunk * kVRow;            // per-key float4 (a_k, b_k, s_v, z_v)
+  static constexpr int kFOff = kVOff + kChunk * kVRow;
   static constexpr int kStage = kFOff + kChunk * 16;
-  static constexpr int kORow = HS + 4;                            // merge buffer row (floats), padded
-  static constexpr int kMergeBytes = 2 * kWaves * NCT * 16 * 4 + NCT * 16 * kORow * 4;
-  static constexpr int kLds = kWaves * kStage > kMergeBytes ? kWaves * kStage : kMergeBytes;
   static_assert(kKDw <= 64 && 64 % kKDw == 0 && kVDw <= 64 && 64 % kVDw == 0, "row layout");
   static_assert(16 % kKpl == 0 && 16 % kVpl == 0, "loads must not straddle a 16-key half chunk");
 };
@@ -85,15 +395,11 @@ struct ChunkRegs {
   uint32_t w;
 };
 
-__device__ __forceinline__ int fast_div(int x, uint32_t magic, uint32_t shift) {
-  return (int)(__umulhi((uint32_t)x, magic) >> shift);
-}
-
-// Loads the 32 keys [k0, k0 + 32) of one KV head into registers. Each 16-key half lies in one cache block (block
-// sizes are multiples of 16); halves at or past kend are skipped.
+// The 32 keys [k0, k0 + 32) of one KV head into registers. Each 16-key half lies in one cache block (block sizes
+// are multiples of 16); halves at or past kend are skipped.
 template <class Sh>
-__device__ __forceinline__ void load_chunk(ChunkRegs<Sh> &r, const DecodeParams &p, const int32_t *trow, int k0,
-                                           int kend, int h, int lane, int koff_lane, int voff_lane) {
+__device__ __forceinline__ void load_rows(ChunkRegs<Sh> &r, const DecodeParams &p, const int32_t *trow, int k0,
+                                          int kend, int h, int lane, int koff_lane, int voff_lane) {
   int bid[2], slot0[2];
   bool valid[2];
 #pragma unroll
@@ -137,9 +443,12 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<Sh> &r, const DecodeParams 
 }
 
 template <int HS, int KFMT, int NCT>
-__global__ __launch_bounds__(256) void decode_kernel(const DecodeParams p) {
-  using Sh = DecodeShape<HS, KFMT, NCT>;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[Sh::kLds];
+__global__ __launch_bounds__(256) void decode_rows_kernel(const DecodeParams p) {
+  constexpr int kWaves = 4;
+  using Sh = RowShape<HS, KFMT>;
+  constexpr int kLds = kWaves * Sh::kStage > merge_lds_bytes<HS, NCT, kWaves>() ? kWaves * Sh::kStage
+                                                                                 : merge_lds_bytes<HS, NCT, kWaves>();
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kLds];
 
   const int lane = threadIdx.x & 63;
   const int w = uniform(threadIdx.x >> 6);
@@ -149,79 +458,30 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeParams p) {
   const int n = p.used_k[seq];
   if (T <= 0 || n <= 0) return;
   const int G = p.num_q_heads / p.num_kv_heads;
-  const int R = T * G;
-  const int seg = (n + p.num_segments * Sh::kChunk - 1) / (p.num_segments * Sh::kChunk) * Sh::kChunk;
+  const int seg = (n + p.num_segments * kChunk - 1) / (p.num_segments * kChunk) * kChunk;
   const int kstart = seg_idx * seg;
   const int kend = min(n, kstart + seg);
   if (kstart >= kend) return;
-
   const int col = lane & 15, g = lane >> 4;
 
-  // ---- query operand (B of S^T = K Q^T): lane holds row col + 16 ct, channels HS/4 * g + 8 mi + perm
-  bf16x8_t qop[NCT][Sh::kNmi];
-  float qsum[NCT];
-  int row_pos[NCT];  // absolute position of the row's query token (causal limit)
-#pragma unroll
-  for (int ct = 0; ct < NCT; ++ct) {
-    const int r = ct * 16 + col;
-    const bool rv = r < R;
-    const int t = (rv ? r : R - 1) / G, j = (rv ? r : R - 1) % G;
-    row_pos[ct] = n - T + t;
-    const uint16_t *qr = p.q + (int64_t)(q0 + t) * p.qs0 + (int64_t)(h * G + j) * p.qs1 + (HS / 4) * g;
-    float qs = 0.f;
-#pragma unroll
-    for (int mi = 0; mi < Sh::kNmi; ++mi) {
-      u32x4_t x = rv ? *reinterpret_cast<const u32x4_t *>(qr + 8 * mi) : u32x4_t{0u, 0u, 0u, 0u};
-      if constexpr (KFMT == QP_CODES_INT4) {
-        // K operand element order per 8 channels: (c0, c4, c1, c5, c2, c6, c3, c7), see nib_pair.
-        qs += bf16_lo(x[0]) + bf16_hi(x[0]) + bf16_lo(x[1]) + bf16_hi(x[1]) + bf16_lo(x[2]) + bf16_hi(x[2]) +
-              bf16_lo(x[3]) + bf16_hi(x[3]);
-        u32x4_t y;
-        y[0] = (x[0] & 0xFFFFu) | (x[2] << 16);
-        y[1] = (x[0] >> 16) | (x[2] & 0xFFFF0000u);
-        y[2] = (x[1] & 0xFFFFu) | (x[3] << 16);
-        y[3] = (x[1] >> 16) | (x[3] & 0xFFFF0000u);
-        qop[ct][mi] = as_bf16x8(y);
-      } else {
-        qop[ct][mi] = as_bf16x8(x);
-      }
-    }
-    if constexpr (KFMT == QP_CODES_INT4) {
-      qs += shfl_xor_f(qs, 16);
-      qs += shfl_xor_f(qs, 32);
-    }
-    qsum[ct] = qs;
-  }
-
-  float m_run[NCT], l_run[NCT], c_run[NCT];
-  f32x4_t acc[NCT][Sh::kNb * 4];
-#pragma unroll
-  for (int ct = 0; ct < NCT; ++ct) {
-    m_run[ct] = -INFINITY;
-    l_run[ct] = 0.f;
-    c_run[ct] = 0.f;
-#pragma unroll
-    for (int i = 0; i < Sh::kNb * 4; ++i) acc[ct][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  }
+  WaveState<HS, KFMT, NCT> st;
+  init_state(st, p, q0, T, n, h, G, col, g);
 
   uint8_t *wl = smem + w * Sh::kStage;
   const int32_t *trow = p.table + (int64_t)seq * p.table_stride;
   const int koff_lane = 4 * (lane % Sh::kKDw) + (lane / Sh::kKDw) * (int)p.ks1;
   const int voff_lane = 4 * (lane % Sh::kVDw) + (lane / Sh::kVDw) * (int)p.vs1;
-  const int nchunks = (kend - kstart + Sh::kChunk - 1) / Sh::kChunk;
-  const int causal_lim = min(kend, n - T + 1);  // keys at or past this need a mask for some row
+  const int nchunks = (kend - kstart + kChunk - 1) / kChunk;
+  const int causal_lim = min(kend, n - T + 1);
 
   ChunkRegs<Sh> regs;
-  if (w < nchunks) load_chunk<Sh>(regs, p, trow, kstart + w * Sh::kChunk, kend, h, lane, koff_lane, voff_lane);
-
-  for (int ci = w; ci < nchunks; ci += Sh::kWaves) {
-    const int k0 = kstart + ci * Sh::kChunk;
-
-    // ---- stage the chunk into this wave's LDS rows
+  if (w < nchunks) load_rows<Sh>(regs, p, trow, kstart + w * kChunk, kend, h, lane, koff_lane, voff_lane);
+  for (int ci = w; ci < nchunks; ci += kWaves) {
+    const int k0 = kstart + ci * kChunk;
 #pragma unroll
     for (int i = 0; i < Sh::kKLoads; ++i) {
       const int kk = Sh::kKpl * i + lane / Sh::kKDw;
-      *reinterpret_cast<uint32_t *>(wl + Sh::kKOff + kk * Sh::kKRow + 4 * (lane % Sh::kKDw)) = regs.k[i];
+      *reinterpret_cast<uint32_t *>(wl + kk * Sh::kKRow + 4 * (lane % Sh::kKDw)) = regs.k[i];
     }
 #pragma unroll
     for (int i = 0; i < Sh::kVLoads; ++i) {
@@ -230,245 +490,145 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeParams p) {
     }
     {
       const int kk = lane & 31;
-      const bool ok = k0 + kk < kend;
-      const uint32_t word = regs.w;
-      float2 f;
-      if (lane < 32) {
-        if constexpr (KFMT == QP_CODES_INT4) {
-          const float a = __uint_as_float(word & 0xFFFFFFF0u) * p.scale_log2;
-          f = make_float2(ok ? a : 0.f, ok ? a * (float)(128u + (word & 0xFu)) : 0.f);
-        } else {
-          f = make_float2(ok ? __uint_as_float(word) * p.scale_log2 : 0.f, 0.f);
-        }
-      } else {
-        f = make_float2(ok ? __uint_as_float(word & 0xFFFFFFF0u) : 0.f, ok ? (float)(128u + (word & 0xFu)) : 0.f);
-      }
+      const float2 f = key_floats<KFMT>(regs.w, lane >= 32, k0 + kk < kend, p.scale_log2);
       *reinterpret_cast<float2 *>(wl + Sh::kFOff + kk * 16 + (lane < 32 ? 0 : 8)) = f;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    wave_sync();
+    if (ci + kWaves < nchunks)
+      load_rows<Sh>(regs, p, trow, k0 + kWaves * kChunk, kend, h, lane, koff_lane, voff_lane);
+    compute_chunk<HS, KFMT, NCT, Sh::kKRow, Sh::kVRow>(st, wl, wl + Sh::kVOff, wl + Sh::kFOff, k0, kend, causal_lim,
+                                                       col, g);
+  }
+  finish_workgroup<HS, KFMT, NCT, kWaves>(st, smem, p, w, col, g, q0, T, G, h, seg_idx);
+}
 
-    // ---- prefetch the wave's next chunk while this one computes
-    if (ci + Sh::kWaves < nchunks)
-      load_chunk<Sh>(regs, p, trow, k0 + Sh::kWaves * Sh::kChunk, kend, h, lane, koff_lane, voff_lane);
+// ------------------------------------------------------- HND page spans: HBM -> LDS direct, double-buffered
+//
+// Cell layout [K codes | K word | V codes | V word] of CELL bytes, slots of one (block, KV head) contiguous: the 16
+// cells of a half chunk are one contiguous run of 16 * CELL bytes (16-byte aligned), copied verbatim into LDS.
 
-    // ---- S^T = K Q^T, two 16-key sub-tiles
-    f32x4_t sacc[NCT][2];
-#pragma unroll
-    for (int st = 0; st < 2; ++st) {
-      const uint8_t *kr = wl + Sh::kKOff + (st * 16 + col) * Sh::kKRow + (Sh::kKeyBytes / 4) * g;
-      if constexpr (KFMT == QP_CODES_INT4) {
-        uint32_t kd[Sh::kNmi];
-#pragma unroll
-        for (int i = 0; i < Sh::kNmi; i += 4) {
-          const u32x4_t v4 = *reinterpret_cast<const u32x4_t *>(kr + 4 * i);
-          kd[i] = v4[0];
-          kd[i + 1] = v4[1];
-          kd[i + 2] = v4[2];
-          kd[i + 3] = v4[3];
-        }
-#pragma unroll
-        for (int mi = 0; mi < Sh::kNmi; ++mi) {
-          const uint32_t x = kd[mi];
-          const bf16x8_t kop =
-              as_bf16x8(u32x4_t{nib_pair(x), nib_pair(x >> 4), nib_pair(x >> 8), nib_pair(x >> 12)});
-#pragma unroll
-          for (int ct = 0; ct < NCT; ++ct)
-            sacc[ct][st] = mfma16x16x32(kop, qop[ct][mi], mi == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sacc[ct][st]);
-        }
-      } else {
-#pragma unroll
-        for (int mi = 0; mi < Sh::kNmi; ++mi) {
-          const u32x2_t x = *reinterpret_cast<const u32x2_t *>(kr + 8 * mi);
-          u32x4_t y;
-#pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            const uint32_t src = x[d >> 1] >> (16 * (d & 1));
-            y[d] = pack_bf16x2((float)(int8_t)(src & 0xFF), (float)(int8_t)(src >> 8));
-          }
-          const bf16x8_t kop = as_bf16x8(y);
-#pragma unroll
-          for (int ct = 0; ct < NCT; ++ct)
-            sacc[ct][st] = mfma16x16x32(kop, qop[ct][mi], mi == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sacc[ct][st]);
-        }
-      }
-    }
+template <int HS, int KFMT>
+struct SpanShape {
+  static constexpr int kKeyBytes = KFMT == QP_CODES_INT4 ? HS / 2 : HS;
+  static constexpr int kCell = kKeyBytes + 4 + HS / 2 + 4;
+  static constexpr int kHalf = 16 * kCell;              // bytes of a 16-key half chunk
+  static constexpr int kUnits = kHalf / 16;             // dwordx4 units per half
+  static constexpr int kFull = kUnits / 64, kRem = kUnits % 64;
+  static constexpr int kDmaPerChunk = 2 * (kFull + (kRem ? 1 : 0));
+  static_assert(kHalf % 16 == 0, "16-byte units");
+};
 
-    // ---- per-key scalars of the lane's 8 keys: 4g + j (sub-tile 0) and 16 + 4g + j (sub-tile 1)
-    float4 kf[2][4];
-#pragma unroll
-    for (int st = 0; st < 2; ++st)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        kf[st][j] = *reinterpret_cast<const float4 *>(wl + Sh::kFOff + (st * 16 + 4 * g + j) * 16);
+// One dwordx4 per lane straight from HBM into LDS at dst + 16 * lane (global_load_lds_dwordx4, LDS base in M0).
+// Issued as inline assembly so that the compiler does not order its own LDS stores behind these copies: every wait
+// on them is placed by hand (wait_vmcnt before a stage is read, wait_lgkm0 before a stage is refilled).
+__device__ __forceinline__ void dma16(const uint8_t *src, uint8_t *dst) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)dst;
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+               : "memory", "m0");
+#endif
+}
 
-    const bool need_mask = k0 + Sh::kChunk > causal_lim;
-#pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) {
-      float s[2][4];
-#pragma unroll
-      for (int st = 0; st < 2; ++st)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if constexpr (KFMT == QP_CODES_INT4)
-            s[st][j] = fmaf(sacc[ct][st][j], kf[st][j].x, -qsum[ct] * kf[st][j].y);
-          else
-            s[st][j] = sacc[ct][st][j] * kf[st][j].x;
-        }
-      if (need_mask) {
-#pragma unroll
-        for (int st = 0; st < 2; ++st)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int key = k0 + st * 16 + 4 * g + j;
-            if (key > row_pos[ct] || key >= kend) s[st][j] = -INFINITY;
-          }
-      }
-      float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
-                       fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
-      mx = fmaxf(mx, shfl_xor_f(mx, 16));
-      mx = fmaxf(mx, shfl_xor_f(mx, 32));
-      if (__any(mx > m_run[ct])) {
-        const float m_new = fmaxf(m_run[ct], mx);
-        const float alpha = m_run[ct] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[ct] - m_new);
-        l_run[ct] *= alpha;
-        c_run[ct] *= alpha;
-#pragma unroll
-        for (int i = 0; i < Sh::kNb * 4; ++i) acc[ct][i] *= alpha;
-        m_run[ct] = m_new;
-      }
-      const float mu = m_run[ct] == -INFINITY ? 0.f : m_run[ct];
-      float lsum = 0.f, csum = 0.f;
-      u32x4_t pw;
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const int st = d >> 1, j0 = (d & 1) * 2;
-        const float p0 = __builtin_amdgcn_exp2f(s[st][j0] - mu);
-        const float p1 = __builtin_amdgcn_exp2f(s[st][j0 + 1] - mu);
-        lsum += p0 + p1;
-        const uint32_t pk = pack_bf16x2(p0 * kf[st][j0].z, p1 * kf[st][j0 + 1].z);
-        csum = fmaf(bf16_lo(pk), kf[st][j0].w, csum);
-        csum = fmaf(bf16_hi(pk), kf[st][j0 + 1].w, csum);
-        pw[d] = pk;
-      }
-      l_run[ct] += lsum;
-      c_run[ct] += csum;
-      // stash the P operand in the (now free) score registers of this row tile
-      sacc[ct][0] = __builtin_bit_cast(f32x4_t, pw);
-    }
+// Two block-table entries through the scalar cache (s_load, lgkm counter). A vector load here would be ordered
+// behind the outstanding HBM -> LDS copies on the vm counter and serialize the pipeline.
+__device__ __forceinline__ void table_pair(const int32_t *trow, int i0, int i1, int &b0, int &b1) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("s_load_dword %0, %2, %3\n\ts_load_dword %1, %2, %4\n\ts_waitcnt lgkmcnt(0)"
+               : "=&s"(b0), "=&s"(b1)
+               : "s"(trow), "s"(i0 * 4), "s"(i1 * 4)
+               : "memory");
+#else
+  b0 = trow[i0];
+  b1 = trow[i1];
+#endif
+}
 
-    // ---- O^T += V^T P^T
+template <class Sh>
+__device__ __forceinline__ void issue_span_dma(const DecodeParams &p, const int32_t *trow, int k0, int kend, int h,
+                                               int lane, uint8_t *stage) {
+  // a half at or past kend re-reads half 0 (valid memory) so that every chunk issues the same count of loads
+  int pos[2], bidx[2], bid[2];
 #pragma unroll
-    for (int b = 0; b < Sh::kNb; ++b) {
-      uint32_t x[4];
+  for (int hc = 0; hc < 2; ++hc) {
+    pos[hc] = uniform(k0 + 16 * ((k0 + 16 * hc < kend) ? hc : 0));
+    bidx[hc] = uniform(fast_div(pos[hc], p.bs_magic, p.bs_shift));
+  }
+  table_pair(trow, bidx[0], bidx[1], bid[0], bid[1]);
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const int ka = (d < 2 ? 4 * g + 2 * d : 16 + 4 * g + 2 * (d - 2));
-        const uint8_t *vr = wl + Sh::kVOff + 2 * (col + 16 * b);
-        const uint32_t lo = *reinterpret_cast<const uint16_t *>(vr + ka * Sh::kVRow);
-        const uint32_t hi = *reinterpret_cast<const uint16_t *>(vr + (ka + 1) * Sh::kVRow);
-        x[d] = lo | (hi << 16);
-      }
+  for (int hc = 0; hc < 2; ++hc) {
+    const int slot0 = pos[hc] - bidx[hc] * p.block_size;
+    const uint8_t *src =
+        p.kcodes + (int64_t)bid[hc] * p.ks0 + (int64_t)h * p.ks2 + (int64_t)slot0 * Sh::kCell + 16 * lane;
+    uint8_t *dst = stage + hc * Sh::kHalf;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        u32x4_t vv;
-#pragma unroll
-        for (int d = 0; d < 4; ++d) vv[d] = nib_pair(x[d] >> (4 * c));
-        const bf16x8_t vop = as_bf16x8(vv);
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct)
-          acc[ct][b * 4 + c] =
-              mfma16x16x32(vop, as_bf16x8(__builtin_bit_cast(u32x4_t, sacc[ct][0])), acc[ct][b * 4 + c]);
-      }
+    for (int i = 0; i < Sh::kFull; ++i) dma16(src + 1024 * i, dst + 1024 * i);
+    if constexpr (Sh::kRem != 0) {
+      if (lane < Sh::kRem) dma16(src + 1024 * Sh::kFull, dst + 1024 * Sh::kFull);
     }
   }
+}
 
-  // ---- finish this wave's rows: sums over the lane groups
-#pragma unroll
-  for (int ct = 0; ct < NCT; ++ct) {
-    l_run[ct] += shfl_xor_f(l_run[ct], 16);
-    l_run[ct] += shfl_xor_f(l_run[ct], 32);
-    c_run[ct] += shfl_xor_f(c_run[ct], 16);
-    c_run[ct] += shfl_xor_f(c_run[ct], 32);
-  }
+template <int HS, int KFMT, int NCT, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodeParams p) {
+  using Sh = SpanShape<HS, KFMT>;
+  constexpr int kStages = 2;
+  constexpr int kCells = WAVES * kStages * 2 * Sh::kHalf;
+  constexpr int kLds = kCells > merge_lds_bytes<HS, NCT, WAVES>() ? kCells : merge_lds_bytes<HS, NCT, WAVES>();
+  // cells (DMA destinations) and per-key scalars live in different allocations, so the compiler can tell the
+  // scalar stores from the in-flight copies and does not wait for the copies before them
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kLds];
+  __shared__ __attribute__((aligned(16))) float4 kfl[WAVES][kStages][kChunk];
 
-  // ---- merge the 4 waves in LDS (staging rows are dead now)
-  __syncthreads();
-  float *st_m = reinterpret_cast<float *>(smem);
-  float *st_l = st_m + Sh::kWaves * NCT * 16;
-  float *obuf = st_l + Sh::kWaves * NCT * 16;
-  if (g == 0) {
-#pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) {
-      st_m[(w * NCT + ct) * 16 + col] = m_run[ct];
-      st_l[(w * NCT + ct) * 16 + col] = l_run[ct];
+  const int lane = threadIdx.x & 63;
+  const int w = uniform(threadIdx.x >> 6);
+  const int seg_idx = blockIdx.x, h = blockIdx.y, seq = blockIdx.z;
+  const int q0 = p.cu_q[seq];
+  const int T = p.cu_q[seq + 1] - q0;
+  const int n = p.used_k[seq];
+  if (T <= 0 || n <= 0) return;
+  const int G = p.num_q_heads / p.num_kv_heads;
+  const int seg = (n + p.num_segments * kChunk - 1) / (p.num_segments * kChunk) * kChunk;
+  const int kstart = seg_idx * seg;
+  const int kend = min(n, kstart + seg);
+  if (kstart >= kend) return;
+  const int col = lane & 15, g = lane >> 4;
+
+  WaveState<HS, KFMT, NCT> st;
+  init_state(st, p, q0, T, n, h, G, col, g);
+
+  uint8_t *wl = smem + w * kStages * 2 * Sh::kHalf;
+  const int32_t *trow = p.table + (int64_t)seq * p.table_stride;
+  const int nchunks = (kend - kstart + kChunk - 1) / kChunk;
+  const int mine = nchunks > w ? (nchunks - w + WAVES - 1) / WAVES : 0;  // chunks of this wave
+  const int causal_lim = min(kend, n - T + 1);
+  constexpr int kWordK = Sh::kKeyBytes, kWordV = Sh::kCell - 4;
+
+  if (mine > 0) issue_span_dma<Sh>(p, trow, kstart + w * kChunk, kend, h, lane, wl);
+  if (mine > 1) issue_span_dma<Sh>(p, trow, kstart + (w + WAVES) * kChunk, kend, h, lane, wl + 2 * Sh::kHalf);
+  for (int i = 0; i < mine; ++i) {
+    const int k0 = kstart + (w + i * WAVES) * kChunk;
+    uint8_t *stage = wl + (i & 1) * 2 * Sh::kHalf;
+    float4 *fl = kfl[w][i & 1];
+    if (i + 1 < mine) wait_vmcnt<Sh::kDmaPerChunk>();
+    else wait_vmcnt<0>();
+    {  // per-key scalars from the words now in LDS
+      const int kk = lane & 31;
+      const bool is_v = lane >= 32;
+      const uint32_t word = *reinterpret_cast<const uint32_t *>(stage + kk * Sh::kCell + (is_v ? kWordV : kWordK));
+      const float2 f = key_floats<KFMT>(word, is_v, k0 + kk < kend, p.scale_log2);
+      *reinterpret_cast<float2 *>(reinterpret_cast<uint8_t *>(fl) + kk * 16 + (is_v ? 8 : 0)) = f;
+    }
+    wave_sync();
+    compute_chunk<HS, KFMT, NCT, Sh::kCell, Sh::kCell>(st, stage, stage + Sh::kKeyBytes + 4,
+                                                       reinterpret_cast<const uint8_t *>(fl), k0, kend, causal_lim,
+                                                       col, g);
+    if (i + 2 < mine) {
+      wait_lgkm0();  // every read of this stage has returned before the DMA may overwrite it
+      wave_sync();
+      issue_span_dma<Sh>(p, trow, k0 + 2 * WAVES * kChunk, kend, h, lane, stage);
     }
   }
-  __syncthreads();
-  float fown[NCT];
-#pragma unroll
-  for (int ct = 0; ct < NCT; ++ct) {
-    float M = -INFINITY;
-#pragma unroll
-    for (int ww = 0; ww < Sh::kWaves; ++ww) M = fmaxf(M, st_m[(ww * NCT + ct) * 16 + col]);
-    fown[ct] = m_run[ct] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[ct] - M);
-  }
-  for (int ww = 0; ww < Sh::kWaves; ++ww) {
-    if (w == ww) {
-#pragma unroll
-      for (int ct = 0; ct < NCT; ++ct) {
-        float *orow = obuf + (ct * 16 + col) * Sh::kORow;
-        const float cr = c_run[ct];
-#pragma unroll
-        for (int b = 0; b < Sh::kNb; ++b)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            float4 v;
-            v.x = (acc[ct][b * 4 + 0][j] - cr) * fown[ct];
-            v.y = (acc[ct][b * 4 + 1][j] - cr) * fown[ct];
-            v.z = (acc[ct][b * 4 + 2][j] - cr) * fown[ct];
-            v.w = (acc[ct][b * 4 + 3][j] - cr) * fown[ct];
-            float4 *dst = reinterpret_cast<float4 *>(orow + 64 * b + 16 * g + 4 * j);
-            if (ww == 0) {
-              *dst = v;
-            } else {
-              const float4 o = *dst;
-              *dst = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
-            }
-          }
-      }
-    }
-    __syncthreads();
-  }
-
-  // ---- write the partial of every valid row
-  for (int idx = threadIdx.x; idx < R * (HS / 4); idx += 256) {
-    const int r = idx / (HS / 4), c4 = idx % (HS / 4);
-    const int t = r / G, j = r % G;
-    float *dst = p.so + (int64_t)(q0 + t) * p.sos0 + (int64_t)(h * G + j) * p.sos1 + (int64_t)seg_idx * p.sos2;
-    reinterpret_cast<float4 *>(dst)[c4] = reinterpret_cast<const float4 *>(obuf + r * Sh::kORow)[c4];
-  }
-  if (w == 0 && g == 0) {
-#pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) {
-      const int r = ct * 16 + col;
-      if (r < R) {
-        float M = -INFINITY, L = 0.f;
-#pragma unroll
-        for (int ww = 0; ww < Sh::kWaves; ++ww) M = fmaxf(M, st_m[(ww * NCT + ct) * 16 + col]);
-#pragma unroll
-        for (int ww = 0; ww < Sh::kWaves; ++ww) {
-          const float mw = st_m[(ww * NCT + ct) * 16 + col];
-          if (mw != -INFINITY) L += st_l[(ww * NCT + ct) * 16 + col] * __builtin_amdgcn_exp2f(mw - M);
-        }
-        const int t = r / G, j = r % G;
-        const int64_t o = (int64_t)(q0 + t) * p.sts0 + (int64_t)(h * G + j) * p.sts1 + seg_idx;
-        p.smax[o] = M;
-        p.ssum[o] = L;
-      }
-    }
-  }
+  finish_workgroup<HS, KFMT, NCT, WAVES>(st, smem, p, w, col, g, q0, T, G, h, seg_idx);
 }
 
 // ------------------------------------------------------------------------------------------------- merge
@@ -488,12 +648,18 @@ struct MergeParams {
   float out_scale;
 };
 
-// One workgroup per (token, query head); thread c owns channel c. With signs, the merged row x is rotated back to
-// (x H D) * out_scale by an in-LDS fast Walsh-Hadamard transform.
+// One workgroup of 256 threads per (token, query head). Thread t reads channels 4 (t % (HS/4)) .. +3 of the
+// segments s = t / (HS/4) + k * (256 / (HS/4)), so every segment row is one coalesced float4 sweep and the loads of
+// different segments are independent; the per-segment weights 2^(m_s - M) are computed once into LDS. With signs,
+// the merged row x is rotated back to (x H D) * out_scale by an in-LDS fast Walsh-Hadamard transform.
 template <bool RHT>
-__global__ __launch_bounds__(1024) void merge_kernel(const MergeParams p) {
-  __shared__ float buf[2][1024];
-  const int tok = blockIdx.x, head = blockIdx.y, c = threadIdx.x;
+__global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
+  constexpr int kMaxSeg = 2048;
+  __shared__ float wts[kMaxSeg];
+  __shared__ float red[256];
+  __shared__ float4 part[256];
+  __shared__ float row[2][1024];
+  const int tok = blockIdx.x, head = blockIdx.y, t = threadIdx.x;
   int lo = 0, hi = p.num_seqs - 1;
   while (lo < hi) {  // last sequence whose first query token is <= tok
     const int mid = (lo + hi + 1) >> 1;
@@ -505,35 +671,84 @@ __global__ __launch_bounds__(1024) void merge_kernel(const MergeParams p) {
   const int active = seg > 0 ? min(p.num_segments, (n + seg - 1) / seg) : 0;
   const float *mrow = p.smax + (int64_t)tok * p.sts0 + (int64_t)head * p.sts1;
   const float *lrow = p.ssum + (int64_t)tok * p.sts0 + (int64_t)head * p.sts1;
-  const float *orow = p.so + (int64_t)tok * p.sos0 + (int64_t)head * p.sos1 + c;
+  // maximum over segments
   float M = -INFINITY;
-  for (int s = 0; s < active; ++s) M = fmaxf(M, mrow[s]);
-  float L = 0.f, a = 0.f;
-  if (M != -INFINITY) {
-    for (int s = 0; s < active; ++s) {
-      const float m = mrow[s];
-      if (m == -INFINITY) continue;
-      const float wgt = __builtin_amdgcn_exp2f(m - M);
-      L = fmaf(lrow[s], wgt, L);
-      a = fmaf(orow[(int64_t)s * p.sos2], wgt, a);
+  for (int s = t; s < active; s += 256) M = fmaxf(M, mrow[s]);
+  red[t] = M;
+  __syncthreads();
+  for (int k = 128; k > 0; k >>= 1) {
+    if (t < k) red[t] = fmaxf(red[t], red[t + k]);
+    __syncthreads();
+  }
+  M = red[0];
+  __syncthreads();
+  // weights and L
+  float L = 0.f;
+  for (int s = t; s < active; s += 256) {
+    const float m = mrow[s];
+    const float wgt = (m == -INFINITY || M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - M);
+    wts[s] = wgt;
+    L = fmaf(lrow[s], wgt, L);
+  }
+  red[t] = L;
+  __syncthreads();
+  for (int k = 128; k > 0; k >>= 1) {
+    if (t < k) red[t] += red[t + k];
+    __syncthreads();
+  }
+  L = red[0];
+  // weighted sum of the segment rows
+  const int quads = p.head_size / 4;
+  const int groups = 256 / quads;
+  const int cq = t % quads, sg = t / quads;
+  float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (sg < groups) {
+    const float *orow = p.so + (int64_t)tok * p.sos0 + (int64_t)head * p.sos1 + 4 * cq;
+#pragma unroll 4
+    for (int s = sg; s < active; s += groups) {
+      const float wgt = wts[s];
+      const float4 v = *reinterpret_cast<const float4 *>(orow + (int64_t)s * p.sos2);
+      a.x = fmaf(v.x, wgt, a.x);
+      a.y = fmaf(v.y, wgt, a.y);
+      a.z = fmaf(v.z, wgt, a.z);
+      a.w = fmaf(v.w, wgt, a.w);
     }
   }
-  float x = L > 0.f ? a / L : 0.f;
+  part[t] = a;
+  __syncthreads();
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  if (t < quads) {
+    float4 s4 = part[t];
+    for (int k = 1; k < groups; ++k) {
+      const float4 o = part[t + k * quads];
+      s4.x += o.x;
+      s4.y += o.y;
+      s4.z += o.z;
+      s4.w += o.w;
+    }
+    row[0][4 * t + 0] = s4.x * inv;
+    row[0][4 * t + 1] = s4.y * inv;
+    row[0][4 * t + 2] = s4.z * inv;
+    row[0][4 * t + 3] = s4.w * inv;
+  }
+  __syncthreads();
+  int cur = 0;
   if constexpr (RHT) {
-    const int hs = p.head_size;
-    int cur = 0;
-    buf[0][c] = x;
-    __syncthreads();
-    for (int span = 1; span < hs; span <<= 1) {
-      const float u = buf[cur][c], v = buf[cur][c ^ span];
-      buf[cur ^ 1][c] = (c & span) ? v - u : u + v;
+    for (int span = 1; span < p.head_size; span <<= 1) {
+      for (int c = t; c < p.head_size; c += 256) {
+        const float u = row[cur][c], v = row[cur][c ^ span];
+        row[cur ^ 1][c] = (c & span) ? v - u : u + v;
+      }
       cur ^= 1;
       __syncthreads();
     }
-    x = buf[cur][c] * p.signs[c] * p.out_scale;
   }
-  p.out[(int64_t)tok * p.os0 + (int64_t)head * p.os1 + c] = f32_to_bf16_bits(x);
-  if (p.lse && c == 0)
+  for (int c = t; c < p.head_size; c += 256) {
+    float x = row[cur][c];
+    if constexpr (RHT) x *= p.signs[c] * p.out_scale;
+    p.out[(int64_t)tok * p.os0 + (int64_t)head * p.os1 + c] = f32_to_bf16_bits(x);
+  }
+  if (p.lse && t == 0)
     p.lse[(int64_t)tok * p.ls0 + (int64_t)head * p.ls1] =
         (M == -INFINITY || L <= 0.f) ? -INFINITY : (M + __log2f(L)) * 0.6931471805599453f;
 }
@@ -553,24 +768,50 @@ void div_magic(uint32_t d, uint32_t *magic, uint32_t *shift) {
   *shift = l - 1;
 }
 
+bool aligned(const void *ptr, uintptr_t a) { return ((uintptr_t)ptr & (a - 1)) == 0; }
+
+// True when the four views are the standard cell layout [K codes | K word | V codes | V word] with the 16-slot runs
+// of each (block, KV head) contiguous and 16-byte aligned: the direct HBM -> LDS span path applies.
+bool is_span_layout(const qp_paged_cache *c) {
+  const int hs = c->head_size;
+  const int kbytes = c->key.format == QP_CODES_INT4 ? hs / 2 : hs;
+  const int64_t cell = kbytes + 4 + hs / 2 + 4;
+  const uint8_t *k = static_cast<const uint8_t *>(c->key.codes);
+  if (static_cast<const uint8_t *>(c->key.words) != k + kbytes) return false;
+  if (static_cast<const uint8_t *>(c->value.codes) != k + kbytes + 4) return false;
+  if (static_cast<const uint8_t *>(c->value.words) != k + kbytes + 4 + hs / 2) return false;
+  for (int i = 0; i < 3; ++i) {
+    if (c->key.code_stride[i] != c->value.code_stride[i]) return false;
+    if (c->key.word_stride[i] * 4 != c->key.code_stride[i] || c->value.word_stride[i] * 4 != c->key.code_stride[i])
+      return false;
+  }
+  if (c->key.code_stride[1] != cell) return false;
+  if (c->key.code_stride[0] % 16 || c->key.code_stride[2] % 16 || !aligned(k, 16)) return false;
+  return (16 * cell) % 16 == 0;
+}
+
 template <int HS, int KFMT, int NCT>
-void launch_decode(const DecodeParams &p, dim3 grid, hipStream_t s) {
-  decode_kernel<HS, KFMT, NCT><<<grid, 256, 0, s>>>(p);
+void launch_decode(const DecodeParams &p, dim3 grid, bool span, hipStream_t s) {
+  if (span) {
+    // 8 waves (2 per SIMD) fit the registers of one row tile with int4 keys; the others run 4.
+    constexpr int kWaves = (KFMT == QP_CODES_INT4 && NCT == 1) ? 8 : 4;
+    decode_span_kernel<HS, KFMT, NCT, kWaves><<<grid, kWaves * 64, 0, s>>>(p);
+  } else {
+    decode_rows_kernel<HS, KFMT, NCT><<<grid, 256, 0, s>>>(p);
+  }
 }
 
 template <int HS>
-int dispatch_decode(const DecodeParams &p, int kfmt, int nct, dim3 grid, hipStream_t s) {
+int dispatch_decode(const DecodeParams &p, int kfmt, int nct, dim3 grid, bool span, hipStream_t s) {
   if (kfmt == QP_CODES_INT4) {
-    if (nct == 1) launch_decode<HS, QP_CODES_INT4, 1>(p, grid, s);
-    else launch_decode<HS, QP_CODES_INT4, 2>(p, grid, s);
+    if (nct == 1) launch_decode<HS, QP_CODES_INT4, 1>(p, grid, span, s);
+    else launch_decode<HS, QP_CODES_INT4, 2>(p, grid, span, s);
   } else {
-    if (nct == 1) launch_decode<HS, QP_CODES_INT8, 1>(p, grid, s);
-    else launch_decode<HS, QP_CODES_INT8, 2>(p, grid, s);
+    if (nct == 1) launch_decode<HS, QP_CODES_INT8, 1>(p, grid, span, s);
+    else launch_decode<HS, QP_CODES_INT8, 2>(p, grid, span, s);
   }
   return launch_status();
 }
-
-bool aligned(const void *ptr, uintptr_t a) { return ((uintptr_t)ptr & (a - 1)) == 0; }
 
 }  // namespace
 
@@ -595,7 +836,7 @@ extern "C" int qp_decode_splitkv(const qp_paged_cache *cache, const qp_decode_ar
   const int G = a->num_q_heads / cache->num_kv_heads;
   const int rows = a->max_query_len * G;
   QP_SUPPORTED(rows <= 32, "qp_decode_splitkv: more than 32 query rows per KV head");
-  QP_REQUIRE(a->num_segments >= 1 && a->num_segments <= 65535, "qp_decode_splitkv: bad segment count");
+  QP_REQUIRE(a->num_segments >= 1 && a->num_segments <= 2048, "qp_decode_splitkv: 1..2048 segments");
   QP_REQUIRE(a->num_tokens <= a->segm_rows, "qp_decode_splitkv: more query tokens than segment-buffer rows");
   QP_REQUIRE(a->num_seqs >= 0 && a->num_seqs <= 65535, "qp_decode_splitkv: bad sequence count");
   for (int i = 0; i < 3; ++i) {
@@ -653,19 +894,24 @@ extern "C" int qp_decode_splitkv(const qp_paged_cache *cache, const qp_decode_ar
   div_magic((uint32_t)cache->block_size, &p.bs_magic, &p.bs_shift);
   p.scale_log2 = a->softmax_scale * kLog2e;
   const int nct = rows > 16 ? 2 : 1;
+  const bool span = is_span_layout(cache) && !getenv("QP_DECODE_ROWS");
   const dim3 grid(a->num_segments, cache->num_kv_heads, a->num_seqs);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (hs == 256) return dispatch_decode<256>(p, cache->key.format, nct, grid, s);
-  return dispatch_decode<128>(p, cache->key.format, nct, grid, s);
+  if (hs == 256) return dispatch_decode<256>(p, cache->key.format, nct, grid, span, s);
+  return dispatch_decode<128>(p, cache->key.format, nct, grid, span, s);
 }
 
 extern "C" int qp_merge_segments(const qp_merge_args *a, qp_stream_t stream) {
   QP_REQUIRE(a && a->segm_output && a->segm_max && a->segm_expsum && a->cu_seqlens_q && a->seqused_k && a->out,
              "qp_merge_segments: null argument");
-  QP_REQUIRE(a->head_size >= 1 && a->head_size <= 1024, "qp_merge_segments: head size must be 1..1024");
+  QP_REQUIRE(a->head_size >= 4 && a->head_size <= 1024 && a->head_size % 4 == 0 && 256 % (a->head_size / 4) == 0,
+             "qp_merge_segments: head size must be 16, 32, 64, ..., 1024");
   QP_REQUIRE(!a->rht_signs || (a->head_size & (a->head_size - 1)) == 0,
              "qp_merge_segments: the fused rotation needs a power-of-two head size");
-  QP_REQUIRE(a->num_segments >= 1 && a->num_seqs >= 1, "qp_merge_segments: bad sizes");
+  QP_REQUIRE(a->num_segments >= 1 && a->num_segments <= 2048 && a->num_seqs >= 1, "qp_merge_segments: bad sizes");
+  QP_REQUIRE(aligned(a->segm_output, 16) && a->segm_output_stride[2] % 4 == 0 && a->segm_output_stride[1] % 4 == 0 &&
+                 a->segm_output_stride[0] % 4 == 0,
+             "qp_merge_segments: segment output rows must be 16-byte aligned");
   if (a->num_tokens == 0) return QP_OK;
   MergeParams p;
   p.so = a->segm_output;
@@ -691,7 +937,7 @@ extern "C" int qp_merge_segments(const qp_merge_args *a, qp_stream_t stream) {
   p.out_scale = a->rht_out_scale;
   const dim3 grid(a->num_tokens, a->num_q_heads);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (a->rht_signs) merge_kernel<true><<<grid, a->head_size, 0, s>>>(p);
-  else merge_kernel<false><<<grid, a->head_size, 0, s>>>(p);
+  if (a->rht_signs) merge_kernel<true><<<grid, 256, 0, s>>>(p);
+  else merge_kernel<false><<<grid, 256, 0, s>>>(p);
   return launch_status();
 }
