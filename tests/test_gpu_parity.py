@@ -268,3 +268,136 @@ def _host_cache(kc, vc, ks, vs, fmt):
     nb, bs, nkv = kc.shape[0], kc.shape[1], kc.shape[2]
     cell = O.int4_cell_bytes(HS) if fmt == "int4" else O.k8v4_cell_bytes(HS)
     return arr.reshape(nb, nkv, bs, cell)
+
+
+# ---------------------------------------------------------------------------------------------------- prefill
+
+def _prefill_case(device, rng, fmt, lens, layout="hnd", bs=16, nq=NQ, nkv=NKV, hs=HS, scale=None):
+    """lens = [(T_i, n_i)]: one batched prefill call; returns (gpu out, emulation, fp64 reference)."""
+    import torch
+
+    from vllm_quantpack.attention import int4_prefill
+    nbs = [-(-n // bs) for _, n in lens]
+    total = sum(nbs) + 2
+    kv, v = random_cache(rng, total, nkv, bs, hs, fmt, layout)
+    _, (kc, vc, ks, vs) = torch_cache(kv, hs, fmt, device)
+    pool = rng.permutation(total).astype(np.int32)
+    table = np.zeros((len(lens), max(nbs)), np.int32)
+    at = 0
+    for i, nb in enumerate(nbs):
+        table[i, :nb] = pool[at:at + nb]
+        at += nb
+    Ts = [t for t, _ in lens]
+    q = O.f32_to_bf16_bits(rng.standard_normal((sum(Ts), nq, hs)).astype(np.float32))
+    cu = np.concatenate(([0], np.cumsum(Ts))).astype(np.int32)
+    scale = scale or hs ** -0.5
+    qt = bf16_tensor(q, device)
+    out = torch.full_like(qt, float("nan"))
+    int4_prefill.prefill_attention(qt, kc, vc, ks, vs, out, cu_seqlens_q=i32(cu, device),
+                                   seqused_k=i32([n for _, n in lens], device), block_table=i32(table, device),
+                                   max_seqlen_q=max(Ts), softmax_scale=scale)
+    torch.cuda.synchronize()
+    qf = O.bf16_bits_to_f32(q)
+    emus, refs = [], []
+    for i, (T, n) in enumerate(lens):
+        qs = qf[cu[i]:cu[i + 1]]
+        emus.append(O.decode_emulated(qs, v, table[i], n, scale, num_segments=1, tile=64))
+        K, V = O.dequant_f64(v, table[i], n)
+        refs.append(O.attention_f64(qs, K, V, n, scale))
+    return to_f32(out), np.concatenate(emus), np.concatenate(refs)
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+@pytest.mark.parametrize("layout", ["hnd", "nhd"])
+def test_prefill_matches_oracle(device, fmt, layout):
+    rng = np.random.default_rng(201)
+    out, emu, ref = _prefill_case(device, rng, fmt, [(100, 3000)], layout=layout)
+    assert np.isfinite(out).all()
+    assert O.relerr(out, emu) < 1e-2
+    assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
+
+
+def test_prefill_varlen_batch(device):
+    """A batch mixing a long chunk, a first chunk (context == chunk), short chunks and single tokens."""
+    rng = np.random.default_rng(202)
+    lens = [(70, 2500), (5, 900), (1, 1), (33, 33), (16, 4000), (17, 64)]
+    out, emu, ref = _prefill_case(device, rng, "int4", lens)
+    at = 0
+    for T, n in lens:
+        sl = slice(at, at + T)
+        assert O.relerr(out[sl], emu[sl]) < 1e-2, (T, n)
+        assert O.relerr(out[sl], ref[sl]) < 5e-3, (T, n)
+        at += T
+
+
+@pytest.mark.parametrize("bs", [32, 3072])
+def test_prefill_block_sizes_and_gqa(device, bs):
+    rng = np.random.default_rng(203 + bs)
+    out, emu, ref = _prefill_case(device, rng, "int4", [(40, 2000)], bs=bs, nq=16, nkv=2, hs=128)
+    assert O.relerr(out, emu) < 1e-2
+    assert O.relerr(out, ref) < 5e-3
+
+
+def test_prefill_span_and_row_loaders_agree(device, monkeypatch):
+    monkeypatch.delenv("QP_PREFILL_ROWS", raising=False)
+    a, emu, ref = _prefill_case(device, np.random.default_rng(204), "int8", [(64, 1500), (3, 700)])
+    monkeypatch.setenv("QP_PREFILL_ROWS", "1")
+    b, _, _ = _prefill_case(device, np.random.default_rng(204), "int8", [(64, 1500), (3, 700)])
+    assert O.relerr(a, emu) < 1e-2 and O.relerr(b, emu) < 1e-2
+    assert O.relerr(a, b) < 5e-3
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+def test_unified_attention_prefill_matches_fp64(device, fmt):
+    """tests/test_int4_kv.py:172-191 prefill rows: a 256-token chunk over a 6000-token context through the router."""
+    import torch
+
+    from vllm_quantpack.attention import int4_kv
+    rng = np.random.default_rng(205)
+    n, bs, qlen = 6000, 16, 256
+    nb = -(-n // bs)
+    kv_np = O.new_cache(nb, NKV, bs, O.int4_cell_bytes(HS) if fmt == "int4" else O.k8v4_cell_bytes(HS))
+    _, (kc, vc, ks, vs) = torch_cache(kv_np, HS, fmt, device)
+    g = torch.Generator(device=device).manual_seed(1)
+    k = torch.randn((n, NKV, HS), generator=g, device=device, dtype=torch.bfloat16)
+    v = torch.randn((n, NKV, HS), generator=g, device=device, dtype=torch.bfloat16)
+    int4_kv.reshape_and_cache_int4(k, v, kc, vc, torch.arange(n, device=device), k_scale_cache=ks,
+                                   v_scale_cache=vs)
+    q = torch.randn((qlen, NQ, HS), generator=g, device=device, dtype=torch.bfloat16)
+    out = torch.empty_like(q)
+    segm = (torch.empty((32, NQ, 16, HS), dtype=torch.float32, device=device),
+            torch.empty((32, NQ, 16), dtype=torch.float32, device=device),
+            torch.empty((32, NQ, 16), dtype=torch.float32, device=device))
+    int4_kv.unified_attention_int4(
+        q, kc, vc, out, cu_seqlens_q=i32([0, qlen], device), max_seqlen_q=qlen, seqused_k=i32([n], device),
+        max_seqlen_k=n, softmax_scale=HS ** -0.5, window_size=(-1, -1),
+        block_table=torch.arange(nb, dtype=torch.int32, device=device)[None], softcap=0.0, sinks=None,
+        alibi_slopes=None, use_alibi_sqrt=False, qq_bias=None, output_scale=None, mm_prefix_range=None,
+        k_scale_cache=ks, v_scale_cache=vs, seq_threshold_3D=32, num_par_softmax_segments=16,
+        softmax_segm_output=segm[0], softmax_segm_max=segm[1], softmax_segm_expsum=segm[2])
+    torch.cuda.synchronize()
+    views = O.int4_views if fmt == "int4" else O.k8v4_views
+    K, V = O.dequant_f64(views(_host_cache(kc, vc, ks, vs, fmt), HS), np.arange(nb), n)
+    qr = O.rht(to_f32(q).astype(np.float64))
+    ref = O.rht(O.attention_f64(qr, K, V, n, HS ** -0.5 / HS), inverse=True) / HS
+    err = O.relerr(to_f32(out), ref)
+    assert err < 5e-3, err
+
+
+def test_prefill_sequence_reference_signature(device):
+    """int4_prefill.prefill_sequence(q_rot, k_cache, v_cache, k_scales, v_scales, block_row, n, scale, fa) as the
+    reference calls it (int4_kv.py:327-328): output in the rotated domain, q_rot's dtype."""
+    import torch
+
+    from vllm_quantpack.attention import int4_prefill
+    rng = np.random.default_rng(206)
+    n, qlen = 2000, 80
+    kv, v = random_cache(rng, -(-n // 16), NKV, 16, HS)
+    _, (kc, vc, ks, vs) = torch_cache(kv, HS, "int4", device)
+    q = O.f32_to_bf16_bits(rng.standard_normal((qlen, NQ, HS)).astype(np.float32))
+    o = int4_prefill.prefill_sequence(bf16_tensor(q, device), kc, vc, ks, vs,
+                                      torch.arange(-(-n // 16), dtype=torch.int32, device=device), n, 0.05, None)
+    assert o.dtype == torch.bfloat16 and tuple(o.shape) == (qlen, NQ, HS)
+    K, V = O.dequant_f64(v, np.arange(-(-n // 16)), n)
+    ref = O.attention_f64(O.bf16_bits_to_f32(q), K, V, n, 0.05)
+    assert O.relerr(to_f32(o), ref) < 5e-3

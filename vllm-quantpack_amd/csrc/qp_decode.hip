@@ -55,24 +55,6 @@ struct DecodeParams {
 
 constexpr int kChunk = QP_DECODE_TILE;  // keys per wave iteration: two 16-key sub-tiles
 
-__device__ __forceinline__ int fast_div(int x, uint32_t magic, uint32_t shift) {
-  return (int)(__umulhi((uint32_t)x, magic) >> shift);
-}
-
-// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
-
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // --------------------------------------------------------------------------------------- per-wave state
 
 template <int HS, int KFMT, int NCT>
@@ -125,20 +107,6 @@ __device__ __forceinline__ void init_state(WaveState<HS, KFMT, NCT> &st, const D
     st.c[ct] = 0.f;
 #pragma unroll
     for (int i = 0; i < HS / 16; ++i) st.acc[ct][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  }
-}
-
-// Per-key scalars of one key from its two words: (a_k, b_k) = (s_k * scale_log2, (128 + zp_k) * a_k) for the key
-// half, (s_v, 128 + zp_v) for the value half; zeros for keys at or past kend.
-template <int KFMT>
-__device__ __forceinline__ float2 key_floats(uint32_t word, bool is_value, bool ok, float scale_log2) {
-  if (!ok) return make_float2(0.f, 0.f);
-  if (is_value) return make_float2(__uint_as_float(word & 0xFFFFFFF0u), (float)(128u + (word & 0xFu)));
-  if constexpr (KFMT == QP_CODES_INT4) {
-    const float a = __uint_as_float(word & 0xFFFFFFF0u) * scale_log2;
-    return make_float2(a, a * (float)(128u + (word & 0xFu)));
-  } else {
-    return make_float2(__uint_as_float(word) * scale_log2, 0.f);
   }
 }
 
@@ -518,31 +486,6 @@ struct SpanShape {
   static_assert(kHalf % 16 == 0, "16-byte units");
 };
 
-// One dwordx4 per lane straight from HBM into LDS at dst + 16 * lane (global_load_lds_dwordx4, LDS base in M0).
-// Issued as inline assembly so that the compiler does not order its own LDS stores behind these copies: every wait
-// on them is placed by hand (wait_vmcnt before a stage is read, wait_lgkm0 before a stage is refilled).
-__device__ __forceinline__ void dma16(const uint8_t *src, uint8_t *dst) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)dst;
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
-               : "memory", "m0");
-#endif
-}
-
-// Two block-table entries through the scalar cache (s_load, lgkm counter). A vector load here would be ordered
-// behind the outstanding HBM -> LDS copies on the vm counter and serialize the pipeline.
-__device__ __forceinline__ void table_pair(const int32_t *trow, int i0, int i1, int &b0, int &b1) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  asm volatile("s_load_dword %0, %2, %3\n\ts_load_dword %1, %2, %4\n\ts_waitcnt lgkmcnt(0)"
-               : "=&s"(b0), "=&s"(b1)
-               : "s"(trow), "s"(i0 * 4), "s"(i1 * 4)
-               : "memory");
-#else
-  b0 = trow[i0];
-  b1 = trow[i1];
-#endif
-}
-
 template <class Sh>
 __device__ __forceinline__ void issue_span_dma(const DecodeParams &p, const int32_t *trow, int k0, int kend, int h,
                                                int lane, uint8_t *stage) {
@@ -758,37 +701,6 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
 using namespace qp;
 
 namespace {
-
-// Exact magic division for 0 <= x < 2^31 by d >= 2: m = ceil(2^(31+l) / d), l = ceil(log2 d); q = umulhi(x, m) >> (l-1).
-void div_magic(uint32_t d, uint32_t *magic, uint32_t *shift) {
-  uint32_t l = 0;
-  while ((1ull << l) < d) ++l;
-  const unsigned __int128 num = (unsigned __int128)1 << (31 + l);
-  *magic = (uint32_t)((num + d - 1) / d);
-  *shift = l - 1;
-}
-
-bool aligned(const void *ptr, uintptr_t a) { return ((uintptr_t)ptr & (a - 1)) == 0; }
-
-// True when the four views are the standard cell layout [K codes | K word | V codes | V word] with the 16-slot runs
-// of each (block, KV head) contiguous and 16-byte aligned: the direct HBM -> LDS span path applies.
-bool is_span_layout(const qp_paged_cache *c) {
-  const int hs = c->head_size;
-  const int kbytes = c->key.format == QP_CODES_INT4 ? hs / 2 : hs;
-  const int64_t cell = kbytes + 4 + hs / 2 + 4;
-  const uint8_t *k = static_cast<const uint8_t *>(c->key.codes);
-  if (static_cast<const uint8_t *>(c->key.words) != k + kbytes) return false;
-  if (static_cast<const uint8_t *>(c->value.codes) != k + kbytes + 4) return false;
-  if (static_cast<const uint8_t *>(c->value.words) != k + kbytes + 4 + hs / 2) return false;
-  for (int i = 0; i < 3; ++i) {
-    if (c->key.code_stride[i] != c->value.code_stride[i]) return false;
-    if (c->key.word_stride[i] * 4 != c->key.code_stride[i] || c->value.word_stride[i] * 4 != c->key.code_stride[i])
-      return false;
-  }
-  if (c->key.code_stride[1] != cell) return false;
-  if (c->key.code_stride[0] % 16 || c->key.code_stride[2] % 16 || !aligned(k, 16)) return false;
-  return (16 * cell) % 16 == 0;
-}
 
 template <int HS, int KFMT, int NCT>
 void launch_decode(const DecodeParams &p, dim3 grid, bool span, hipStream_t s) {
