@@ -129,8 +129,12 @@ int qp_merge_segments(const qp_merge_args *args, qp_stream_t stream);
  * Chunked-prefill attention of a batch of sequences over the paged cache, causal within each sequence's query
  * chunk: K/V tiles are dequantised to exact bf16 integers in LDS and QK^T / PV run on bf16 MFMA with an online
  * softmax; out is bf16. Any number of query tokens per sequence; no host synchronisation.
- * Replaces prefill_sequence (int4_prefill.py:203-232: unpack to bf16 segments + FlashAttention + LSE merge) and the
- * 2D path of the generated Triton kernel (int4_kv.py:113-118).
+ * When the query blocks alone cannot fill the device, the keys of each block are split over workgroups
+ * (num_splits, 0 = chosen for the device) whose fp32 partials go to the caller's workspace and are merged as in
+ * qp_merge_segments; without enough workspace an automatic choice falls back to one split.
+ * With rht_signs the result is rotated back, out = (o H D) * rht_out_scale, as qp_merge_segments does.
+ * Replaces prefill_sequence (int4_prefill.py:203-232: unpack to bf16 segments + FlashAttention + LSE merge, with the
+ * inverse single_rht of int4_kv.py:329) and the 2D path of the generated Triton kernel (int4_kv.py:113-118).
  */
 typedef struct qp_prefill_args {
   const void *query;           /* bf16 [num_tokens, num_q_heads, head_size] */
@@ -143,12 +147,21 @@ typedef struct qp_prefill_args {
   int32_t num_tokens;
   int32_t num_q_heads;
   int32_t max_query_len;
+  int32_t max_seqlen_k;        /* longest context: bounds the automatic split count (0: no splits) */
+  int32_t num_splits;          /* key splits per query block; 0 = automatic */
   float softmax_scale;
   void *out;                   /* bf16 [num_tokens, num_q_heads, head_size] */
   int64_t out_stride[2];
+  void *workspace;             /* >= qp_prefill_workspace_size bytes, 16-byte aligned; may be NULL */
+  int64_t workspace_bytes;
+  const float *rht_signs;      /* optional: inverse rotation of the output (needs a contiguous out) */
+  float rht_out_scale;
 } qp_prefill_args;
 
 int qp_prefill(const qp_paged_cache *cache, const qp_prefill_args *args, qp_stream_t stream);
+
+/* Workspace bytes qp_prefill uses for these arguments on the current device (0 when it does not split). */
+int64_t qp_prefill_workspace_size(const qp_paged_cache *cache, const qp_prefill_args *args);
 
 /*
  * Quantise-and-store of new keys/values into the paged cache: per (token, KV head) keys to int4 (asymmetric

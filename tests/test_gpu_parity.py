@@ -272,21 +272,30 @@ def _host_cache(kc, vc, ks, vs, fmt):
 
 # ---------------------------------------------------------------------------------------------------- prefill
 
-def _prefill_case(device, rng, fmt, lens, layout="hnd", bs=16, nq=NQ, nkv=NKV, hs=HS, scale=None):
-    """lens = [(T_i, n_i)]: one batched prefill call; returns (gpu out, emulation, fp64 reference)."""
+def _prefill_case(device, rng, fmt, lens, layout="hnd", bs=16, nq=NQ, nkv=NKV, hs=HS, scale=None, splits=0,
+                  big_keys=()):
+    """lens = [(T_i, n_i)]: one batched prefill call; returns (gpu out, emulation, fp64 reference). big_keys =
+    [(position, scale)] gives those key positions of every sequence a large key scale (scores far above the first
+    tile's maximum)."""
     import torch
 
     from vllm_quantpack.attention import int4_prefill
     nbs = [-(-n // bs) for _, n in lens]
     total = sum(nbs) + 2
     kv, v = random_cache(rng, total, nkv, bs, hs, fmt, layout)
-    _, (kc, vc, ks, vs) = torch_cache(kv, hs, fmt, device)
     pool = rng.permutation(total).astype(np.int32)
     table = np.zeros((len(lens), max(nbs)), np.int32)
     at = 0
     for i, nb in enumerate(nbs):
         table[i, :nb] = pool[at:at + nb]
         at += nb
+    for pos, sc in big_keys:
+        for i in range(len(lens)):
+            blk, slot = table[i, pos // bs], pos % bs
+            words = v.key_word[blk, slot]
+            bits = np.float32(sc).view(np.uint32) & np.uint32(0xFFFFFFF0)
+            words[:] = (words & np.uint32(0xF)) | bits if fmt == "int4" else np.float32(sc).view(np.uint32)
+    _, (kc, vc, ks, vs) = torch_cache(kv, hs, fmt, device)
     Ts = [t for t, _ in lens]
     q = O.f32_to_bf16_bits(rng.standard_normal((sum(Ts), nq, hs)).astype(np.float32))
     cu = np.concatenate(([0], np.cumsum(Ts))).astype(np.int32)
@@ -295,7 +304,7 @@ def _prefill_case(device, rng, fmt, lens, layout="hnd", bs=16, nq=NQ, nkv=NKV, h
     out = torch.full_like(qt, float("nan"))
     int4_prefill.prefill_attention(qt, kc, vc, ks, vs, out, cu_seqlens_q=i32(cu, device),
                                    seqused_k=i32([n for _, n in lens], device), block_table=i32(table, device),
-                                   max_seqlen_q=max(Ts), softmax_scale=scale)
+                                   max_seqlen_q=max(Ts), softmax_scale=scale, num_splits=splits)
     torch.cuda.synchronize()
     qf = O.bf16_bits_to_f32(q)
     emus, refs = [], []
@@ -315,6 +324,57 @@ def test_prefill_matches_oracle(device, fmt, layout):
     assert np.isfinite(out).all()
     assert O.relerr(out, emu) < 1e-2
     assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 5])
+def test_prefill_key_splits_agree(device, splits):
+    """Keys split over 1, 2 or 5 workgroups per query block and merged: the same attention (the split ranges follow
+    the split-KV segment rule, so some sequences get empty splits)."""
+    rng = np.random.default_rng(210)
+    lens = [(48, 2600), (7, 300), (33, 33)]
+    out, emu, ref = _prefill_case(device, rng, "int4", lens, splits=splits)
+    assert np.isfinite(out).all()
+    assert O.relerr(out, emu) < 1e-2
+    assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+def test_prefill_scores_far_above_the_first_tile(device, fmt):
+    """Keys with scales 2^7 .. 2^12 late in the context push scores thousands of log2 units above the first tile's
+    maximum: the workgroup raises its maximum and redoes its keys, and the result still matches."""
+    rng = np.random.default_rng(211)
+    big = [(700, 2.0 ** 7), (1300, 2.0 ** 9), (1901, 2.0 ** 12)]
+    out, emu, ref = _prefill_case(device, rng, fmt, [(40, 2000), (9, 1400)], splits=1, big_keys=big)
+    assert np.isfinite(out).all()
+    assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
+
+
+def test_prefill_fused_rotation(device):
+    """rht_signs rotates the output back inside the library, with and without key splits."""
+    import torch
+
+    from vllm_quantpack.attention import int4_prefill, rht
+    rng = np.random.default_rng(212)
+    n, qlen, bs = 3000, 64, 16
+    nb = -(-n // bs)
+    kv, v = random_cache(rng, nb, NKV, bs, HS)
+    _, (kc, vc, ks, vs) = torch_cache(kv, HS, "int4", device)
+    q = O.f32_to_bf16_bits(rng.standard_normal((qlen, NQ, HS)).astype(np.float32))
+    qt = bf16_tensor(q, device)
+    table = torch.arange(nb, dtype=torch.int32, device=device)[None]
+    signs = rht.signs(HS, device)
+    plain = torch.empty_like(qt)
+    int4_prefill.prefill_attention(qt, kc, vc, ks, vs, plain, cu_seqlens_q=i32([0, qlen], device),
+                                   seqused_k=i32([n], device), block_table=table, max_seqlen_q=qlen,
+                                   softmax_scale=0.06, num_splits=1)
+    want = O.rht(to_f32(plain).astype(np.float64), inverse=True) / HS
+    for splits in (1, 3):
+        got = torch.empty_like(qt)
+        int4_prefill.prefill_attention(qt, kc, vc, ks, vs, got, cu_seqlens_q=i32([0, qlen], device),
+                                       seqused_k=i32([n], device), block_table=table, max_seqlen_q=qlen,
+                                       softmax_scale=0.06, num_splits=splits, rht_signs=signs, rht_out_scale=1 / HS)
+        torch.cuda.synchronize()
+        assert O.relerr(to_f32(got), want) < 1e-2, splits
 
 
 def test_prefill_varlen_batch(device):

@@ -56,7 +56,9 @@ class PrefillArgs(Structure):
     _fields_ = [("query", c_void_p), ("query_stride", I64x2), ("cu_seqlens_q", c_void_p), ("seqused_k", c_void_p),
                 ("block_table", c_void_p), ("block_table_stride", c_int64), ("num_seqs", c_int32),
                 ("num_tokens", c_int32), ("num_q_heads", c_int32), ("max_query_len", c_int32),
-                ("softmax_scale", c_float), ("out", c_void_p), ("out_stride", I64x2)]
+                ("max_seqlen_k", c_int32), ("num_splits", c_int32), ("softmax_scale", c_float), ("out", c_void_p),
+                ("out_stride", I64x2), ("workspace", c_void_p), ("workspace_bytes", c_int64),
+                ("rht_signs", c_void_p), ("rht_out_scale", c_float)]
 
 
 class StoreArgs(Structure):
@@ -71,6 +73,7 @@ SIGNATURES = {
     "qp_decode_splitkv": (c_int32, [POINTER(PagedCache), POINTER(DecodeArgs), c_void_p]),
     "qp_merge_segments": (c_int32, [POINTER(MergeArgs), c_void_p]),
     "qp_prefill": (c_int32, [POINTER(PagedCache), POINTER(PrefillArgs), c_void_p]),
+    "qp_prefill_workspace_size": (c_int64, [POINTER(PagedCache), POINTER(PrefillArgs)]),
     "qp_store": (c_int32, [POINTER(PagedCache), POINTER(StoreArgs), c_void_p]),
     "qp_rht": (c_int32, [c_void_p, c_int32, c_int64, c_void_p, c_int32, c_int64, c_int64, c_int32, c_void_p,
                          c_int32, c_float, c_void_p]),

@@ -107,7 +107,7 @@ def unified_attention_int4(q, k_cache, v_cache, out, *, cu_seqlens_q, max_seqlen
 
     Split-KV decode when every sequence has <= MAX_Q_SPLIT_KV query tokens, q fits the segment buffers and the GQA
     group times the tokens fits one workgroup (int4_kv.py:101-112); the batched MFMA prefill kernel otherwise."""
-    del max_seqlen_k, use_alibi_sqrt, seq_threshold_3D, kw
+    del use_alibi_sqrt, seq_threshold_3D, kw
     _plain(q, window_size, softcap, sinks, alibi_slopes, qq_bias, output_scale, mm_prefix_range)
     hs = q.shape[2]
     scale = float(softmax_scale) / hs           # <R q, R k> = hs <q, k>
@@ -128,11 +128,14 @@ def unified_attention_int4(q, k_cache, v_cache, out, *, cu_seqlens_q, max_seqlen
         if target is not out:
             out.copy_(target)
         return None
-    o_rot = torch.empty_like(q_rot)
-    int4_prefill.prefill_attention(q_rot, k_cache, v_cache, k_scale_cache, v_scale_cache, o_rot,
+    # the prefill kernel (or its split merge) rotates the result back itself
+    target = out if (out.dtype == torch.bfloat16 and out.is_contiguous()) else torch.empty_like(q)
+    int4_prefill.prefill_attention(q_rot, k_cache, v_cache, k_scale_cache, v_scale_cache, target,
                                    cu_seqlens_q=cu_seqlens_q, seqused_k=seqused_k, block_table=block_table,
-                                   max_seqlen_q=max_seqlen_q, softmax_scale=scale)
-    out.copy_(single_rht(o_rot, inverse=True, out_dtype=torch.float32, out_scale=1.0 / hs))
+                                   max_seqlen_q=max_seqlen_q, softmax_scale=scale, max_seqlen_k=max_seqlen_k,
+                                   rht_signs=signs, rht_out_scale=1.0 / hs)
+    if target is not out:
+        out.copy_(target)
     return None
 
 

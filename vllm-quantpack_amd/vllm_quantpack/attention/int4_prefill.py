@@ -48,17 +48,45 @@ def _cu_seqlens(length: int, device) -> torch.Tensor:
 
 
 def prefill_attention(q, k_cache, v_cache, k_scale_cache, v_scale_cache, out, *, cu_seqlens_q, seqused_k,
-                      block_table, max_seqlen_q, softmax_scale) -> None:
+                      block_table, max_seqlen_q, softmax_scale, max_seqlen_k=None, num_splits=0, rht_signs=None,
+                      rht_out_scale=1.0) -> None:
     """Batched causal attention of the query tokens of every sequence (the last cu_seqlens_q[i+1] - cu_seqlens_q[i]
     positions of a context of seqused_k[i] tokens) over the paged cache: q and out bf16 [T, NQ, hs] in the cache's
-    domain, softmax_scale multiplies q.k in that domain."""
+    domain, softmax_scale multiplies q.k in that domain. With rht_signs the result is rotated back,
+    out = (o H D) * rht_out_scale. When the chunk alone cannot fill the GPU, the keys are split over workgroups
+    (num_splits, 0 = automatic) and merged; the fp32 partials go to a workspace from torch's caching allocator.
+    max_seqlen_k bounds the automatic split count; without it the block table's capacity stands in (no host sync)."""
     hs = q.shape[2]
     cache = _hip.paged_cache(k_cache, v_cache, k_scale_cache, v_scale_cache, hs)
-    args = _hip.PrefillArgs(q.data_ptr(), _hip.I64x2(q.stride(0), q.stride(1)), cu_seqlens_q.data_ptr(),
-                            seqused_k.data_ptr(), block_table.data_ptr(), block_table.stride(0),
-                            len(seqused_k), q.shape[0], q.shape[1], int(max_seqlen_q), float(softmax_scale),
-                            out.data_ptr(), _hip.I64x2(out.stride(0), out.stride(1)))
-    _hip.check(_hip.lib().qp_prefill(cache, args, _hip.stream_of(q)), "prefill")
+    if max_seqlen_k is None:
+        max_seqlen_k = block_table.shape[1] * k_cache.shape[1]
+    args = _hip.PrefillArgs()
+    args.query = q.data_ptr()
+    args.query_stride = _hip.I64x2(q.stride(0), q.stride(1))
+    args.cu_seqlens_q = cu_seqlens_q.data_ptr()
+    args.seqused_k = seqused_k.data_ptr()
+    args.block_table = block_table.data_ptr()
+    args.block_table_stride = block_table.stride(0)
+    args.num_seqs = len(seqused_k)
+    args.num_tokens = q.shape[0]
+    args.num_q_heads = q.shape[1]
+    args.max_query_len = int(max_seqlen_q)
+    args.max_seqlen_k = int(min(max_seqlen_k, 2**31 - 1))
+    args.num_splits = int(num_splits)
+    args.softmax_scale = float(softmax_scale)
+    args.out = out.data_ptr()
+    args.out_stride = _hip.I64x2(out.stride(0), out.stride(1))
+    args.rht_signs = _hip.ptr(rht_signs)
+    args.rht_out_scale = float(rht_out_scale)
+    lib = _hip.lib()
+    need = lib.qp_prefill_workspace_size(cache, args)
+    if num_splits and num_splits > 1:
+        rows = q.shape[0] * q.shape[1] * num_splits
+        need = rows * hs * 4 + 2 * rows * 4
+    ws = torch.empty(need, dtype=torch.uint8, device=q.device) if need > 0 else None
+    args.workspace = _hip.ptr(ws)
+    args.workspace_bytes = need
+    _hip.check(lib.qp_prefill(cache, args, _hip.stream_of(q)), "prefill")
 
 
 def prefill_sequence(q_rot, k_cache, v_cache, k_scales, v_scales, block_row, n, softmax_scale, fa=None):
@@ -80,6 +108,9 @@ def prefill_sequence(q_rot, k_cache, v_cache, k_scales, v_scales, block_row, n, 
     return out if q_rot.dtype == torch.bfloat16 else out.to(q_rot.dtype)
 
 
-# The reference's single-kernel INT8-QK alternative (int4_prefill.py:176-200) has the same contract; the MFMA kernel
-# serves both names.
-prefill_sequence_i8 = prefill_sequence
+def prefill_sequence_i8(q_rot, k_cache, v_cache, k_scales, v_scales, block_row, n, softmax_scale, block_m=64,
+                        block_n=64, num_warps=8, num_stages=2):
+    """The reference's single-kernel alternative with the same contract as prefill_sequence (int4_prefill.py:176-200);
+    its tile arguments are accepted and not used: the MFMA kernel serves both names, with the exact arithmetic."""
+    del block_m, block_n, num_warps, num_stages
+    return prefill_sequence(q_rot, k_cache, v_cache, k_scales, v_scales, block_row, n, softmax_scale)
