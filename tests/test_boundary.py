@@ -217,3 +217,31 @@ def test_unsupported_features_raise():
         int4_kv._plain(q, (128, 0), 0.0, None, None, None, None, None)
     with pytest.raises(NotImplementedError, match="softcap"):
         int4_kv._plain(q, (-1, -1), 30.0, None, None, None, None, None)
+
+
+def _build_module():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("qp_build", os.path.join(REPO, "vllm-quantpack_amd", "build.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_inline_mfma_wait_scan():
+    """The build's scan flags a read of an inline-assembly MFMA result inside the wait window and nothing else."""
+    scan = _build_module().mfma_hazards
+    mfma = "v_mfma_f32_16x16x32_bf16 a[0:3], v[4:7], v[8:11], a[0:3]"
+    early = f";;#ASMSTART\n\t{mfma}\n;;#ASMEND\n\tv_accvgpr_read_b32 v1, a2\n"
+    assert len(scan(early)) == 1
+    waited = f";;#ASMSTART\n\t{mfma}\n\ts_nop 7\n\ts_nop 7\n\ts_nop 1\n;;#ASMEND\n\tv_accvgpr_read_b32 v1, a2\n"
+    assert scan(waited) == []
+    # an accumulating MFMA on the same registers is ordered by the hardware; one reading them as srcA is not
+    chained = f";;#ASMSTART\n\t{mfma}\n\t{mfma}\n\ts_nop 7\n\ts_nop 7\n\ts_nop 1\n;;#ASMEND\n"
+    assert scan(chained) == []
+    srca = f";;#ASMSTART\n\t{mfma}\n;;#ASMEND\n\tv_mfma_f32_16x16x32_bf16 v[0:3], a[0:3], v[8:11], 0\n"
+    assert len(scan(srca)) == 1
+    # the compiler's own MFMAs are left to its hazard recognizer
+    assert scan("\tv_mfma_f32_16x16x32_bf16 v[0:3], v[4:7], v[8:11], 0\n\tv_mov_b32 v9, v1\n") == []
+    # a VGPR destination too
+    vdst = ";;#ASMSTART\n\tv_mfma_f32_16x16x32_bf16 v[20:23], v[4:7], v[8:11], v[20:23]\n;;#ASMEND\n\tv_mov_b32 v0, v21\n"
+    assert len(scan(vdst)) == 1

@@ -6,6 +6,7 @@ the Python package so that it travels with the source tree).
 import argparse
 import concurrent.futures as cf
 import os
+import re
 import subprocess
 import sys
 
@@ -28,9 +29,17 @@ def hipcc():
     return path if os.path.exists(path) else "hipcc"
 
 
+# Per-source extra flags. The prefill kernel keeps its QK^T MFMA results in VGPRs (its PV accumulators own the AGPRs).
+EXTRA = {"qp_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
+def _flags(src):
+    return FLAGS + EXTRA.get(os.path.basename(src), [])
+
+
 def _compile(src, verbose):
     obj = os.path.join(OBJ, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [hipcc(), *FLAGS, "-c", src, "-o", obj]
+    cmd = [hipcc(), *_flags(src), "-c", src, "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -39,13 +48,92 @@ def _compile(src, verbose):
     return obj
 
 
+# Inline-assembly MFMAs are invisible to the compiler's hazard recognizer: it does not know that their results land
+# some cycles after issue, and may read them (a copy of its own, for instance) too early. The kernels place the
+# required wait states inside their assembly; this scan of the generated code checks that nothing reads or writes the
+# destination of an inline-assembly MFMA within MFMA_WAIT wait states (each intervening instruction counted as one,
+# s_nop N as N + 1), except a following MFMA that accumulates into exactly the same registers (srcC = vdst, which the
+# hardware orders). The compiler's own MFMAs are covered by its hazard recognizer.
+MFMA_WAIT = 18
+_REG = re.compile(r"\b([va])\[(\d+):(\d+)\]|\b([va])(\d+)\b")
+
+
+def _vregs(text):
+    """VGPRs and AGPRs named in an operand list, as ('v', n) / ('a', n)."""
+    out = set()
+    for m in _REG.finditer(text):
+        if m.group(4) is not None:
+            out.add((m.group(4), int(m.group(5))))
+        else:
+            out.update((m.group(1), r) for r in range(int(m.group(2)), int(m.group(3)) + 1))
+    return out
+
+
+def mfma_hazards(asm):
+    """[(line, mfma, reader)] of too-early accesses to the results of inline-assembly MFMAs (those between the
+    compiler's ;;#ASMSTART / ;;#ASMEND markers) in one assembly listing."""
+    ins = []
+    inline = False
+    for i, raw in enumerate(asm.splitlines()):
+        l = raw.strip()
+        if l.startswith(";;#ASMSTART"):
+            inline = True
+        elif l.startswith(";;#ASMEND"):
+            inline = False
+        elif l and not l.startswith((";", ".")) and not raw.startswith((".", "_")):
+            ins.append((i, l.split(";")[0].strip(), inline))
+    found = []
+    for k, (i, line, inl) in enumerate(ins):
+        if not (inl and line.startswith("v_mfma")):
+            continue
+        regs = _vregs(line.split(None, 1)[1].split(",")[0])
+        waits = 0
+        for _, nxt, _ in ins[k + 1:k + 1 + MFMA_WAIT]:
+            if waits >= MFMA_WAIT:
+                break
+            op = nxt.split()[0]
+            if op == "s_nop":
+                waits += int(nxt.split()[1]) + 1
+                continue
+            args = nxt.split(None, 1)[1] if " " in nxt else ""
+            if op.startswith("v_mfma"):
+                ops = [a.strip() for a in args.split(",")]
+                if _vregs(ops[0]) == regs and _vregs(ops[3]) == regs and not regs & _vregs(",".join(ops[1:3])):
+                    waits += 1
+                    continue
+            if regs & _vregs(args):
+                found.append((i, line, nxt))
+                break
+            waits += 1
+    return found
+
+
+def _check_inline_mfma(src, verbose):
+    text = open(src).read()
+    if 'asm volatile("v_mfma' not in text:
+        return
+    out = os.path.join(OBJ, os.path.basename(src).replace(".hip", ".gfx.s"))
+    cmd = [hipcc(), *_flags(src), "--cuda-device-only", "-S", src, "-o", out]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc -S failed on {src}:\n{r.stdout}\n{r.stderr}")
+    bad = mfma_hazards(open(out).read())
+    if bad:
+        lines = "\n".join(f"  {a}: {b}  ->  {c}" for a, b, c in bad[:10])
+        raise RuntimeError(f"{src}: MFMA results read within {MFMA_WAIT} wait states:\n{lines}")
+
+
 def build(jobs=None, verbose=False):
-    """Compile every csrc/*.hip and link the shared library. Returns the library path."""
+    """Compile every csrc/*.hip, check the inline-MFMA wait states and link the shared library. Returns the library
+    path."""
     os.makedirs(OBJ, exist_ok=True)
     srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
     jobs = jobs or min(8, os.cpu_count() or 1, len(srcs))
     with cf.ThreadPoolExecutor(jobs) as ex:
         objs = list(ex.map(lambda s: _compile(s, verbose), srcs))
+        list(ex.map(lambda s: _check_inline_mfma(s, verbose), srcs))
     tmp = LIB + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     if verbose:

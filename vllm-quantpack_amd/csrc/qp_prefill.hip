@@ -26,6 +26,8 @@
 // (acc, m, l) in the split-KV layout and qp_merge_segments combines them (with the inverse rotation when asked).
 #include "qp_common.h"
 
+#include <type_traits>
+
 namespace qp {
 
 struct PrefillParams {
@@ -56,6 +58,7 @@ struct PrefillParams {
 constexpr int kPfKeys = 32;  // keys per tile
 constexpr int kPfWaves = 4;
 constexpr float kPfRescale = 64.f;  // log2 headroom before the running maximum is raised
+constexpr int kPfMaxPasses = 8;     // passes over a split's keys (restarts after a raised maximum) at most
 
 template <int HS, int KFMT>
 struct PfShape {
@@ -69,27 +72,32 @@ struct PfShape {
   static constexpr int kKdRow = HS * 2 + 16;                 // bf16 K row, padded: conflict-free 16 B reads
   static constexpr int kVtRow = kPfKeys * 2 + 16;            // bf16 V^T row
   static constexpr int kVtRows = HS + 16;                    // + the zero-point tile
-  static constexpr int kKd = kPfKeys * kKdRow;
+  static constexpr int kKd = kPfKeys * kKdRow;               // one K buffer
   static constexpr int kVt = kVtRows * kVtRow;
-  static constexpr int kKf = 3 * kPfKeys * 4 + 16;  // a_k, e_k, s_v + a dummy slot
-  static constexpr int kBuf = kKd + kVt + kKf;
-  static constexpr int kOffBuf = 3 * kPk;
-  static constexpr int kLds = kOffBuf + 2 * kBuf;
-  static_assert(kKd % 16 == 0 && kVt % 16 == 0 && kBuf % 16 == 0, "alignment");
+  static constexpr int kKf = 3 * kPfKeys * 4 + 16;           // a_k, e_k, s_v + a dummy slot
+  static constexpr int kVb = kVt + kKf;                      // one V buffer: V^T rows, then the per-key scalars
+  static constexpr int kOffK = 3 * kPk;                      // 3 packed slots, 2 K buffers, 3 V buffers
+  static constexpr int kOffV = kOffK + 2 * kKd;
+  static constexpr int kLds = kOffV + 3 * kVb;
+  static_assert(kKd % 16 == 0 && kVt % 16 == 0 && kVb % 16 == 0, "alignment");
   static_assert(kLds <= 160 * 1024, "LDS");
 };
 
 // Copies the packed cells of keys [k0, k0 + 32) into slot pk: 16-byte unit u of the tile image (run u / kRunUnits,
 // cells back to back) goes to pk + 16 u. Wave w's copy i covers units 64 (4 i + w) + lane; units past the image
 // re-read unit 0 into the padding. A run at or past kend re-reads run 0, so only valid blocks are addressed.
+// Block-table indices of the two page runs of the tile at key k0 (a run at or past kend repeats run 0).
+__device__ __forceinline__ void pf_runs(const PrefillParams &p, int k0, int kend, int &key1, int &b0, int &b1) {
+  key1 = uniform(k0 + 16 < kend ? k0 + 16 : k0);
+  b0 = uniform(fast_div(k0, p.bs_magic, p.bs_shift));
+  b1 = uniform(fast_div(key1, p.bs_magic, p.bs_shift));
+}
+
 template <class Sh>
-__device__ __forceinline__ void pf_issue(const PrefillParams &p, const int32_t *trow, int k0, int kend, int h, int w,
-                                         int lane, uint8_t *pk) {
-  const int key1 = uniform(k0 + 16 < kend ? k0 + 16 : k0);
-  const int b0 = uniform(fast_div(k0, p.bs_magic, p.bs_shift));
-  const int b1 = uniform(fast_div(key1, p.bs_magic, p.bs_shift));
-  int bid0, bid1;
-  table_pair(trow, b0, b1, bid0, bid1);
+__device__ __forceinline__ void pf_issue_ids(const PrefillParams &p, int k0, int kend, int bid0, int bid1, int h,
+                                             int w, int lane, uint8_t *pk) {
+  int key1, b0, b1;
+  pf_runs(p, k0, kend, key1, b0, b1);
   const uint8_t *run0 =
       p.kcodes + (int64_t)bid0 * p.ks0 + (int64_t)h * p.ks2 + (int64_t)(k0 - b0 * p.block_size) * Sh::kCell;
   const uint8_t *run1 =
@@ -102,6 +110,15 @@ __device__ __forceinline__ void pf_issue(const PrefillParams &p, const int32_t *
         u < Sh::kRunUnits ? run0 + 16 * u : (u < Sh::kTileUnits ? run1 + 16 * (u - Sh::kRunUnits) : run0);
     dma16(src, pk + 1024 * chunk);
   }
+}
+
+template <class Sh>
+__device__ __forceinline__ void pf_issue(const PrefillParams &p, const int32_t *trow, int k0, int kend, int h, int w,
+                                         int lane, uint8_t *pk) {
+  int key1, b0, b1, bid0, bid1;
+  pf_runs(p, k0, kend, key1, b0, b1);
+  table_pair(trow, b0, b1, bid0, bid1);
+  pf_issue_ids<Sh>(p, k0, kend, bid0, bid1, h, w, lane, pk);
 }
 
 // Strided fallback: the same packed image gathered dword by dword through VGPRs (any 4-byte aligned views).
@@ -213,12 +230,12 @@ __device__ __forceinline__ void pf_unpack_v(const uint8_t *pk, uint8_t *vt, int 
 template <int HS, int NT>
 struct PfRows {
   bf16x8_t qop[NT][HS / 32];
-  f32x4_t acc[NT][HS / 16 + 1];  // O^T tiles: tile b row j -> channel 16 b + 4 g + j; tile HS/16 row 0 = zp sum
+  f32x4_t acc[NT][17];  // O^T tiles: tile b row j -> channel 16 b + 4 g + j; tile HS/16 row 0 = zp sum (17 = 256 / 16 + 1)
   float qsum[NT], m[NT], l[NT];
   int row_pos[NT];
 };
 
-// The unpack of one tile cut into stages that pf_step spreads over its MFMA steps (each stage is a few LDS operations
+// The unpack of one tile cut into stages that pf_step_fast spreads over its MFMA steps (each stage is a few LDS operations
 // and VALU ops, so the MFMA pipe stays busy while they issue). Same results as pf_unpack_k + pf_unpack_v.
 template <int HS, int KFMT>
 struct PfStager {
@@ -298,212 +315,229 @@ struct PfStager {
   }
 };
 
-// QK^T MFMAs issued as inline assembly with VGPR results: the scores feed the VALU softmax, and leaving this chain to
-// the compiler would put it in the AGPR file next to the PV accumulators, where the allocator shuffles registers every
-// tile. The compiler does not see these as MFMAs, so the waits it would insert are placed here: qk_settle holds the
-// VALU back until the last results have landed (an 8-pass XDL write needs 11 wait states before a VALU read; 18 are
-// given), accumulation into the previous result of the same chain is ordered by the hardware, and the chains of a
-// wave are interleaved, so at least two other MFMAs sit between dependent ones.
-__device__ __forceinline__ f32x4_t qk_first(bf16x8_t a, bf16x8_t b) {
-  f32x4_t d;
-  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
-  return d;
-}
-__device__ __forceinline__ void qk_next(f32x4_t &d, bf16x8_t a, bf16x8_t b) {
-  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
-}
+// MFMA register files. QK^T runs on compiler-visible MFMAs whose scores land in VGPRs (this file is built with
+// -amdgpu-mfma-vgpr-form): the softmax reads them, and the compiler inserts the waits its hazard rules require. The PV
+// accumulators (NT x 17 tiles, up to 204 registers) must stay in AGPRs, and the compiler keeps them there only when
+// nothing else competes for that file: PV therefore runs as inline-assembly MFMAs with AGPR operands (pv_step), which
+// only other PV MFMAs touch until the epilogue. The compiler cannot see those as MFMAs; their results are read by
+// the next accumulation of the same tile (ordered by the hardware) and, after the last tile, by the epilogue, so the
+// last PV step of every tile ends with 18 wait states (an 8-pass XDL result needs 11 before any other read). The build
+// scans the generated code for any access to an MFMA destination within 18 wait states and fails if it finds one.
 template <int NT>
-__device__ __forceinline__ void qk_settle(f32x4_t (&s)[NT][2]) {
+__device__ __forceinline__ void pv_step(f32x4_t (&acc)[NT][17], int b, bf16x8_t vop, const u32x4_t (&pop)[NT],
+                                        bool last) {
+  static_assert(NT >= 1 && NT <= 3, "row tiles");
+  // (the accumulator array is sized for head 256; head 128 uses tiles 0..8)
   if constexpr (NT == 1) {
-    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 1" : "+v"(s[0][0]), "+v"(s[0][1]));
+    if (last)
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 1"
+                   : "+a"(acc[0][b]) : "v"(vop), "v"(pop[0]));
+    else
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc[0][b]) : "v"(vop), "v"(pop[0]));
   } else if constexpr (NT == 2) {
-    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 1" : "+v"(s[0][0]), "+v"(s[0][1]), "+v"(s[1][0]), "+v"(s[1][1]));
+    if (last)
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %2, %3, %0\n\tv_mfma_f32_16x16x32_bf16 %1, %2, %4, %1\n\t"
+                   "s_nop 7\n\ts_nop 7\n\ts_nop 1"
+                   : "+a"(acc[0][b]), "+a"(acc[1][b]) : "v"(vop), "v"(pop[0]), "v"(pop[1]));
+    else
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %2, %3, %0\n\tv_mfma_f32_16x16x32_bf16 %1, %2, %4, %1"
+                   : "+a"(acc[0][b]), "+a"(acc[1][b]) : "v"(vop), "v"(pop[0]), "v"(pop[1]));
   } else {
-    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 1"
-                 : "+v"(s[0][0]), "+v"(s[0][1]), "+v"(s[1][0]), "+v"(s[1][1]), "+v"(s[2][0]), "+v"(s[2][1]));
+    if (last)
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %3, %4, %0\n\tv_mfma_f32_16x16x32_bf16 %1, %3, %5, %1\n\t"
+                   "v_mfma_f32_16x16x32_bf16 %2, %3, %6, %2\n\ts_nop 7\n\ts_nop 7\n\ts_nop 1"
+                   : "+a"(acc[0][b]), "+a"(acc[1][b]), "+a"(acc[2][b])
+                   : "v"(vop), "v"(pop[0]), "v"(pop[1]), "v"(pop[2]));
+    else
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %3, %4, %0\n\tv_mfma_f32_16x16x32_bf16 %1, %3, %5, %1\n\t"
+                   "v_mfma_f32_16x16x32_bf16 %2, %3, %6, %2"
+                   : "+a"(acc[0][b]), "+a"(acc[1][b]), "+a"(acc[2][b])
+                   : "v"(vop), "v"(pop[0]), "v"(pop[1]), "v"(pop[2]));
   }
 }
 
-// One 32-key tile for the wave's NT row tiles from buffer cur, with the unpack of the next tile (packed slot pkn into
-// buffer nxt) staged over the MFMA steps. Every step is fenced from the next (sched_barrier), so operand loads run a
-// fixed distance ahead (3 steps) instead of all at once, which keeps the registers in flight bounded.
+// one QK step (32 channels of one 16-key sub-tile) for every row tile of the wave
+template <int HS, int NT>
+__device__ __forceinline__ void qk_step(f32x4_t (&d)[NT][2], int sub, int mi, bf16x8_t kop,
+                                        const bf16x8_t (&qop)[NT][HS / 32]) {
+#pragma unroll
+  for (int j = 0; j < NT; ++j)
+    d[j][sub] = mfma16x16x32(kop, qop[j][mi], mi == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : d[j][sub]);
+}
+
+// S^T of one tile for all row tiles of the wave (prologue of a pass).
 template <int HS, int KFMT, int NT>
-__device__ __forceinline__ void pf_step(PfRows<HS, NT> &r, const uint8_t *cur, int k0, int kend, bool masked,
-                                        bool first, int *restart, const uint8_t *pkn, uint8_t *nxt, int k0n,
-                                        int kendn, float scale_log2, int tid, int col, int g) {
+__device__ __forceinline__ void pf_qk_tile(const PfRows<HS, NT> &r, const uint8_t *kd, f32x4_t (&sacc)[NT][2],
+                                           int col, int g) {
+  using Sh = PfShape<HS, KFMT>;
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    const uint8_t *kr = kd + (16 * sub + col) * Sh::kKdRow + 2 * (HS / 4) * g;
+#pragma unroll
+    for (int mi = 0; mi < HS / 32; ++mi) {
+      const bf16x8_t kop = *reinterpret_cast<const bf16x8_t *>(kr + 16 * mi);
+      qk_step<HS, NT>(sacc, sub, mi, kop, r.qop);
+    }
+  }
+}
+
+// The running maximum of a pass starts from the first tile's scores, so that every tile can subtract it without a
+// row reduction.
+template <int HS, int KFMT, int NT>
+__device__ __forceinline__ void pf_initial_max(PfRows<HS, NT> &r, const f32x4_t (&sacc)[NT][2], const uint8_t *vb,
+                                               int k0, int kend, bool masked, int g) {
+  using Sh = PfShape<HS, KFMT>;
+  const float *kf = reinterpret_cast<const float *>(vb + Sh::kVt);
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    float rm = -INFINITY;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const float4 a = *reinterpret_cast<const float4 *>(kf + 16 * sub + 4 * g);
+      const float4 e = *reinterpret_cast<const float4 *>(kf + kPfKeys + 16 * sub + 4 * g);
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        float v;
+        if constexpr (KFMT == QP_CODES_INT4) v = fmaf(sacc[j][sub][jj], a[jj], -(r.qsum[j] * e[jj]));
+        else v = sacc[j][sub][jj] * a[jj];
+        const int key = k0 + 16 * sub + 4 * g + jj;
+        if (masked && (key > r.row_pos[j] || key >= kend)) v = -INFINITY;
+        rm = fmaxf(rm, v);
+      }
+    }
+    rm = fmaxf(rm, shfl_xor_f(rm, 16));
+    rm = fmaxf(rm, shfl_xor_f(rm, 32));
+    r.m[j] = fmaxf(r.m[j], rm);
+  }
+}
+
+// One pipeline iteration, software-pipelined across tiles so that the MFMA pipe always has work next to the VALU:
+//   phase A: S^T of tile i + 1 (K from kd1; 3 MFMAs per K operand, one per row tile)
+//            + softmax of tile i (scores sprev, scalars from vb0) + the K part of tile i + 2's unpack;
+//   phase B: O^T += V^T P^T of tile i (V^T from vb0) + the V part of tile i + 2's unpack.
+// Each phase is a sequence of MFMA steps fenced by sched_barrier, the operand loads running a fixed distance ahead.
+// A score beyond the headroom only posts a restart request (the tile index) for the next barrier.
+template <int HS, int KFMT, int NT, bool MASK>
+__device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev)[NT][2], f32x4_t (&snew)[NT][2],
+                                        const uint8_t *kd1, const uint8_t *vb0, int k0, int kend,
+                                        int *restart, int it, bool may_restart, PfStager<HS, KFMT> &st, int col,
+                                        int g) {
   using Sh = PfShape<HS, KFMT>;
   using St = PfStager<HS, KFMT>;
-  constexpr int kQSteps = 2 * (HS / 32);  // (16-key sub-tile, 32-channel step)
-  constexpr int kPSteps = HS / 16 + 1;    // channel tiles + the zero-point tile
+  constexpr int kMi = HS / 32;     // 32-channel steps per 16-key sub-tile
+  constexpr int kQ = 2 * kMi;      // K operands per tile
+  constexpr int kP = HS / 16 + 1;  // V^T operands (channel tiles + the zero-point tile)
   constexpr int kPre = 3;
-  static_assert(St::kNK + 2 < kQSteps, "K unpack stages must fit the QK steps");
-  const uint8_t *kd = cur;
-  const uint8_t *vt = cur + Sh::kKd;
-  const float *kf = reinterpret_cast<const float *>(cur + Sh::kKd + Sh::kVt);
-  St st;
-  st.pk = pkn;
-  st.kd = nxt;
-  st.vt = nxt + Sh::kKd;
-  st.k0 = k0n;
-  st.kend = kendn;
-  st.tid = tid;
-  st.scale_log2 = scale_log2;
+  constexpr int kSm = 7;           // softmax work items per row tile
+  static_assert(St::kNK * 2 <= kQ, "K unpack stages must fit phase A");
+  const float *kf = reinterpret_cast<const float *>(vb0 + Sh::kVt);
 
-  // ---- S^T = K Q^T for the wave's row tiles, next tile's K rows unpacked alongside
-  auto kaddr = [&](int s) {
-    return kd + (16 * (s / (HS / 32)) + col) * Sh::kKdRow + 2 * (HS / 4) * g + 16 * (s % (HS / 32));
+  auto kaddr = [&](int s) { return kd1 + (16 * (s / kMi) + col) * Sh::kKdRow + 2 * (HS / 4) * g + 16 * (s % kMi); };
+  auto vaddr = [&](int b) { return vb0 + (16 * b + col) * Sh::kVtRow + 16 * g; };
+  bf16x8_t kbuf[kPre], vbuf[kPre];
+  float4 ka[2], ke[2], ks[2];
+  float t[NT][2][4], mx[NT], lsum[NT];
+  u32x4_t pop[NT];
+  bool trig = false;
+
+  // softmax of row tile j, item k: 0-1 scores of sub-tile k, 2 the headroom check, 3-6 probabilities of 2 keys
+  auto sm_item = [&](int j, int k) {
+    if (k < 2) {
+      const int sub = k;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        float c;
+        if constexpr (KFMT == QP_CODES_INT4) c = fmaf(r.qsum[j], ke[sub][jj], r.m[j]);
+        else c = r.m[j];
+        t[j][sub][jj] = fmaf(sprev[j][sub][jj], ka[sub][jj], -c);
+      }
+      if constexpr (MASK) {
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int key = k0 + 16 * sub + 4 * g + jj;
+          if (key > r.row_pos[j] || key >= kend) t[j][sub][jj] = -INFINITY;
+        }
+      }
+    } else if (k == 2) {
+      mx[j] = fmaxf(fmaxf(fmaxf(t[j][0][0], t[j][0][1]), fmaxf(t[j][0][2], t[j][0][3])),
+                    fmaxf(fmaxf(t[j][1][0], t[j][1][1]), fmaxf(t[j][1][2], t[j][1][3])));
+      trig = trig || __any(mx[j] > kPfRescale);
+      lsum[j] = 0.f;
+    } else {
+      const int sub = (k - 3) >> 1, h2 = (k - 3) & 1;
+      const float p0 = __builtin_amdgcn_exp2f(t[j][sub][2 * h2]);
+      const float p1 = __builtin_amdgcn_exp2f(t[j][sub][2 * h2 + 1]);
+      lsum[j] += p0 + p1;
+      pop[j][2 * sub + h2] = pack_bf16x2(p0 * ks[sub][2 * h2], p1 * ks[sub][2 * h2 + 1]);
+      if (k == kSm - 1) r.l[j] += lsum[j];
+    }
   };
-  bf16x8_t kbuf[kPre];
+
+  // ---- phase A
 #pragma unroll
   for (int s = 0; s < kPre; ++s) kbuf[s] = *reinterpret_cast<const bf16x8_t *>(kaddr(s));
-  float4 ka[2], ke[2], ks[2];
-  f32x4_t sacc[NT][2];
 #pragma unroll
-  for (int s = 0; s < kQSteps; ++s) {
-    const int sub = s / (HS / 32), mi = s % (HS / 32);
+  for (int sb = 0; sb < 2; ++sb) {
+    ka[sb] = *reinterpret_cast<const float4 *>(kf + 16 * sb + 4 * g);
+    if constexpr (KFMT == QP_CODES_INT4) ke[sb] = *reinterpret_cast<const float4 *>(kf + kPfKeys + 16 * sb + 4 * g);
+    ks[sb] = *reinterpret_cast<const float4 *>(kf + 2 * kPfKeys + 16 * sb + 4 * g);
+  }
+#pragma unroll
+  for (int s = 0; s < kQ; ++s) {
+    const int sub = s / kMi, mi = s % kMi;
     const bf16x8_t kop = kbuf[s % kPre];
-    if (s + kPre < kQSteps) kbuf[s % kPre] = *reinterpret_cast<const bf16x8_t *>(kaddr(s + kPre));
-#pragma unroll
-    for (int j = 0; j < NT; ++j)
-      if (mi == 0) sacc[j][sub] = qk_first(kop, r.qop[j][mi]);
-      else qk_next(sacc[j][sub], kop, r.qop[j][mi]);
+    if (s + kPre < kQ) kbuf[s % kPre] = *reinterpret_cast<const bf16x8_t *>(kaddr(s + kPre));
+    qk_step<HS, NT>(snew, sub, mi, kop, r.qop);
     if (s < St::kNK) st.k_load(s);
-    if (s >= 2 && s - 2 < St::kNK) st.k_store(s - 2);
-    if (s == kQSteps - 2) {
+    if (s >= St::kNK && s < 2 * St::kNK) st.k_store(s - St::kNK);
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-        ka[sb] = *reinterpret_cast<const float4 *>(kf + 16 * sb + 4 * g);
-        if constexpr (KFMT == QP_CODES_INT4) ke[sb] = *reinterpret_cast<const float4 *>(kf + kPfKeys + 16 * sb + 4 * g);
-        ks[sb] = *reinterpret_cast<const float4 *>(kf + 2 * kPfKeys + 16 * sb + 4 * g);
-      }
+    for (int q = 0; q < NT * kSm; ++q) {
+      const int at = 1 + q * (kQ - 1) / (NT * kSm);
+      if (s == at) sm_item(q / kSm, q % kSm);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  qk_settle(sacc);
-
-  // ---- scores relative to the running maximum: t = S - m = raw a_k - (qsum e_k + m), 2 VALU ops
-  float t[NT][2][4];
-  auto raw_score = [&](int j, int sub, int jj) {
-    float v;
-    if constexpr (KFMT == QP_CODES_INT4) v = fmaf(sacc[j][sub][jj], ka[sub][jj], -(r.qsum[j] * ke[sub][jj]));
-    else v = sacc[j][sub][jj] * ka[sub][jj];
-    const int key = k0 + 16 * sub + 4 * g + jj;
-    return (masked && (key > r.row_pos[j] || key >= kend)) ? -INFINITY : v;
-  };
-  auto raise_max = [&]() {
-    // m = max(m, row maximum of this tile's scores); acc and l are not touched here
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      float rm = -INFINITY;
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          t[j][sub][jj] = raw_score(j, sub, jj);
-          rm = fmaxf(rm, t[j][sub][jj]);
-        }
-      rm = fmaxf(rm, shfl_xor_f(rm, 16));
-      rm = fmaxf(rm, shfl_xor_f(rm, 32));
-      r.m[j] = fmaxf(r.m[j], rm);
-      const float mu = r.m[j] == -INFINITY ? 0.f : r.m[j];
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) t[j][sub][jj] -= mu;
-    }
-  };
-  if (first) {
-    // first tile of a pass: acc and l are still zero, so the maximum is taken from this tile directly
-    raise_max();
-  } else {
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < NT; ++j)
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          float c;
-          if constexpr (KFMT == QP_CODES_INT4) c = fmaf(r.qsum[j], ke[sub][jj], r.m[j]);
-          else c = r.m[j];
-          t[j][sub][jj] = fmaf(sacc[j][sub][jj], ka[sub][jj], -c);
-        }
-    if (masked) {
-#pragma unroll
-      for (int j = 0; j < NT; ++j)
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            const int key = k0 + 16 * sub + 4 * g + jj;
-            if (key > r.row_pos[j] || key >= kend) t[j][sub][jj] = -INFINITY;
-          }
-    }
-#pragma unroll
-    for (int j = 0; j < NT; ++j)
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) mx = fmaxf(mx, t[j][sub][jj]);
-    if (__builtin_expect(__any(mx > kPfRescale), 0)) {
-      // a score beyond the headroom: raise the maximum and have the workgroup redo its keys from the start (the
-      // accumulators are only ever written by MFMAs, which keeps them resident in AGPRs)
-      raise_max();
-      *restart = 1;
-    }
-  }
-
-  // ---- P = 2^t; l from the unrounded P; P^T operand = bf16(P s_v) in K-slot order
-  auto vaddr = [&](int b) { return vt + (16 * b + col) * Sh::kVtRow + 16 * g; };
-  bf16x8_t vbuf[kPre];
+  // ---- phase B
 #pragma unroll
   for (int b = 0; b < kPre; ++b) vbuf[b] = *reinterpret_cast<const bf16x8_t *>(vaddr(b));
-  u32x4_t pop[NT];
+  auto at = [&](int b, int x) { return b == (x < kP - 1 ? x : kP - 1); };
 #pragma unroll
-  for (int j = 0; j < NT; ++j) {
-    float lsum = 0.f;
-    uint32_t w[4];
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const float p0 = __builtin_amdgcn_exp2f(t[j][sub][2 * h2]);
-        const float p1 = __builtin_amdgcn_exp2f(t[j][sub][2 * h2 + 1]);
-        lsum += p0 + p1;
-        w[2 * sub + h2] = pack_bf16x2(p0 * ks[sub][2 * h2], p1 * ks[sub][2 * h2 + 1]);
-      }
-    r.l[j] += lsum;
-    pop[j] = u32x4_t{w[0], w[1], w[2], w[3]};
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
-  // ---- O^T += V^T P^T (channel tiles + the zero-point tile), next tile's V^T and scalars unpacked alongside
-  auto at = [&](int s, int x) { return s == (x < kPSteps - 1 ? x : kPSteps - 1); };
-#pragma unroll
-  for (int b = 0; b < kPSteps; ++b) {
+  for (int b = 0; b < kP; ++b) {
     const bf16x8_t vop = vbuf[b % kPre];
-    if (b + kPre < kPSteps) vbuf[b % kPre] = *reinterpret_cast<const bf16x8_t *>(vaddr(b + kPre));
-#pragma unroll
-    for (int j = 0; j < NT; ++j) r.acc[j][b] = mfma16x16x32(vop, as_bf16x8(pop[j]), r.acc[j][b]);
+    if (b + kPre < kP) vbuf[b % kPre] = *reinterpret_cast<const bf16x8_t *>(vaddr(b + kPre));
+    pv_step<NT>(r.acc, b, vop, pop, b == kP - 1);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       if (at(b, q)) st.v_load(q);
     if (at(b, 1)) st.s_load();
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      if (at(b, q + 2)) st.v_perm(q);
-    if (at(b, 3)) st.s_store();
+      if (at(b, q + 4)) st.v_perm(q);
+    if (at(b, 5)) st.s_store();
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      if (at(b, c + 6)) st.v_store(c);
+      if (at(b, c + 8)) st.v_store(c);
     __builtin_amdgcn_sched_barrier(0);
+  }
+
+  if (__builtin_expect(trig && may_restart, 0)) {
+    // some score is far above the running maximum: raise it (scores = t + m) and ask for a restart of the pass
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      float rm = mx[j];
+      rm = fmaxf(rm, shfl_xor_f(rm, 16));
+      rm = fmaxf(rm, shfl_xor_f(rm, 32));
+      if (rm > 0.f) r.m[j] += rm;
+    }
+    *restart = it;
   }
 }
 
 template <int HS, int KFMT, int NT, bool SPAN>
 __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillParams p) {
   using Sh = PfShape<HS, KFMT>;
+  using St = PfStager<HS, KFMT>;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[Sh::kLds];
 
   const int tid = threadIdx.x;
@@ -577,75 +611,129 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
   const int ntiles = ke > kb ? (ke - kb + kPfKeys - 1) / kPfKeys : 0;
   const int vis_all = first_pos + 1;  // keys below this are visible to every row of the block
 
-  uint8_t *pk_base = smem;
-  uint8_t *bufs = smem + Sh::kOffBuf;
+  // tile t: packed slot t % 3, K buffer t % 2, V buffer t % 3
+  auto pk_of = [&](int t) { return smem + (t % 3) * Sh::kPk; };
+  auto kd_of = [&](int t) { return smem + Sh::kOffK + (t & 1) * Sh::kKd; };
+  auto vb_of = [&](int t) { return smem + Sh::kOffV + (t % 3) * Sh::kVb; };
+  auto tile_key = [&](int t) { return kb + t * kPfKeys; };
+  auto fetch = [&](int t) {  // packed image of tile t into its slot
+    if constexpr (SPAN) pf_issue<Sh>(p, trow, tile_key(t), ke, h, w, lane, pk_of(t));
+    else pf_gather<Sh>(p, trow, tile_key(t), ke, h, pk_of(t));
+  };
   __shared__ int restart;
-  // rows HS + 1 .. HS + 15 of both V^T tiles (the zero-point tile's unused rows) stay zero
+  constexpr int kNoRestart = 0x7fffffff;
+  // rows HS + 1 .. HS + 15 of every V^T tile (the zero-point tile's unused rows) stay zero
   constexpr int kZeroDw = 15 * (Sh::kVtRow / 4);
-  for (int i = tid; i < 2 * kZeroDw; i += kPfWaves * 64)
-    reinterpret_cast<uint32_t *>(bufs + (i / kZeroDw) * Sh::kBuf + Sh::kKd + (HS + 1) * Sh::kVtRow)[i % kZeroDw] = 0u;
-  if (tid == 0) restart = 0;
+  for (int i = tid; i < 3 * kZeroDw; i += kPfWaves * 64)
+    reinterpret_cast<uint32_t *>(smem + Sh::kOffV + (i / kZeroDw) * Sh::kVb + (HS + 1) * Sh::kVtRow)[i % kZeroDw] = 0u;
+  if (tid == 0) restart = kNoRestart;
 
   // A pass runs over the split's keys with the running maximum m; if a score exceeds m by the headroom, m is raised and
-  // the pass starts over (acc and l restart from zero; m keeps its value). Realistic inputs take one pass.
-  for (;;) {
-    const bf16x8_t zero = as_bf16x8(u32x4_t{0u, 0u, 0u, 0u});
+  // the pass starts over (acc and l restart from zero; m keeps its value). Realistic inputs take one pass; each restart
+  // needs scores 2^64 above the last maximum, and after kPfMaxPasses the pass runs to the end whatever it sees (only
+  // non-finite or adversarial scales get there).
+  for (int pass = 0;; ++pass) {
 #pragma unroll
     for (int jt = 0; jt < NT; ++jt) {
       r.l[jt] = 0.f;
-      // zeroed by an MFMA (0 * 0 + 0): every definition of acc is an MFMA result, so acc stays in AGPRs
 #pragma unroll
-      for (int b = 0; b <= HS / 16; ++b) r.acc[jt][b] = mfma16x16x32(zero, zero, f32x4_t{0.f, 0.f, 0.f, 0.f});
+      for (int b = 0; b <= HS / 16; ++b) r.acc[jt][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
     if (ntiles == 0) break;
-    // prologue: tiles 0 and 1 in flight, tile 0 unpacked into buffer 0, tile 2 in flight
+    // ---- prologue: tiles 0..2 fetched, 0 and 1 unpacked, tile 3 fetched, S(0) and the initial maximum
+    fetch(0);
+    if (ntiles > 1) fetch(1);
+    if (ntiles > 2) fetch(2);
     if constexpr (SPAN) {
-      pf_issue<Sh>(p, trow, kb, ke, h, w, lane, pk_base);
-      if (ntiles > 1) {
-        pf_issue<Sh>(p, trow, kb + kPfKeys, ke, h, w, lane, pk_base + Sh::kPk);
-        wait_vmcnt<Sh::kDmaPerWave>();
-      } else {
-        wait_vmcnt<0>();
-      }
-    } else {
-      pf_gather<Sh>(p, trow, kb, ke, h, pk_base);
+      if (ntiles > 2) wait_vmcnt<2 * Sh::kDmaPerWave>();
+      else if (ntiles > 1) wait_vmcnt<Sh::kDmaPerWave>();
+      else wait_vmcnt<0>();
     }
     __syncthreads();
+    pf_unpack_k<HS, KFMT>(pk_of(0), kd_of(0), tid);
+    pf_unpack_v<HS, KFMT>(pk_of(0), vb_of(0), tile_key(0), ke, p.scale_log2, tid);
     if constexpr (SPAN) {
-      if (ntiles > 2) pf_issue<Sh>(p, trow, kb + 2 * kPfKeys, ke, h, w, lane, pk_base + 2 * Sh::kPk);
+      if (ntiles > 2) wait_vmcnt<Sh::kDmaPerWave>();
+      else wait_vmcnt<0>();
     }
-    pf_unpack_k<HS, KFMT>(pk_base, bufs, tid);
-    pf_unpack_v<HS, KFMT>(pk_base, bufs + Sh::kKd, kb, ke, p.scale_log2, tid);
+    __syncthreads();  // tile 0 unpacked; slot 0 free; tile 1 landed
+    if (ntiles > 3) fetch(3);
+    if (ntiles > 1) {
+      pf_unpack_k<HS, KFMT>(pk_of(1), kd_of(1), tid);
+      pf_unpack_v<HS, KFMT>(pk_of(1), vb_of(1), tile_key(1), ke, p.scale_log2, tid);
+    }
+    f32x4_t sprev[NT][2], snew[NT][2];
+    pf_qk_tile<HS, KFMT, NT>(r, kd_of(0), sprev, col, g);
+    pf_initial_max<HS, KFMT, NT>(r, sprev, vb_of(0), tile_key(0), ke, tile_key(0) + kPfKeys > vis_all, g);
 
+    // block ids of tile 4, fetched a tile ahead of its copy through the scalar cache (constant address space: the
+    // compiler issues s_load and places the lgkm wait itself, and the vm counter of the copies is left alone)
+    const __attribute__((address_space(4))) int32_t *ctab = (const __attribute__((address_space(4))) int32_t *)trow;
+    int nb0 = 0, nb1 = 0;
+    auto table_ahead = [&](int t) {
+      int key1, b0, b1;
+      pf_runs(p, tile_key(t), ke, key1, b0, b1);
+      nb0 = ctab[b0];
+      nb1 = ctab[b1];
+    };
+    if (SPAN && ntiles > 4) table_ahead(4);
+
+    // One pipeline iteration; false when a restart was requested. Tiles whose keys are all visible to every row come
+    // first and run without the causal mask; the rest (the chunk's own keys) run with it.
     bool again = false;
-    for (int it = 0; it < ntiles; ++it) {
-      const int k0 = kb + it * kPfKeys;
-      const bool more = it + 1 < ntiles;
-      // past the last tile the "next" unpack reads a stale slot into the idle buffer: same code path, no branch
-      uint8_t *pk_next = pk_base + ((it + 1) % 3) * Sh::kPk;
+    auto iteration = [&](int it, auto mask_tag) -> bool {
+      constexpr bool kMask = decltype(mask_tag)::value;
       if constexpr (SPAN) {
-        if (it + 2 < ntiles) wait_vmcnt<Sh::kDmaPerWave>();
+        if (it + 3 < ntiles) wait_vmcnt<Sh::kDmaPerWave>();
         else wait_vmcnt<0>();
-      } else {
-        if (more) pf_gather<Sh>(p, trow, k0 + kPfKeys, ke, h, pk_next);
       }
-      __syncthreads();  // tile it unpacked by all; tile it + 1 landed; tile it - 1's buffer and slot are free
-      if (restart) {
+      __syncthreads();  // tile it + 1 unpacked by all; tile it + 2 landed; tile it's K and it - 1's V buffers free
+      if (restart < it) return false;  // a wave asked during an earlier tile (every such write precedes the barrier)
+      if (it + 4 < ntiles) {  // into slot (it + 1) % 3, unpacked before this barrier
+        if constexpr (SPAN) {
+          pf_issue_ids<Sh>(p, tile_key(it + 4), ke, nb0, nb1, h, w, lane, pk_of(it + 4));
+          if (it + 5 < ntiles) table_ahead(it + 5);
+        } else {
+          fetch(it + 4);
+        }
+      }
+      // past the last tiles, the stage unpacks a stale slot into idle buffers: same code path, no branch
+      St st;
+      st.pk = pk_of(it + 2);
+      st.kd = kd_of(it + 2);
+      st.vt = vb_of(it + 2);
+      st.k0 = tile_key(it + 2);
+      st.kend = ke;
+      st.tid = tid;
+      st.scale_log2 = p.scale_log2;
+      pf_iter<HS, KFMT, NT, kMask>(r, sprev, snew, kd_of(it + 1), vb_of(it), tile_key(it), ke, &restart, it,
+                                   pass + 1 < kPfMaxPasses, st, col, g);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        sprev[j][0] = snew[j][0];
+        sprev[j][1] = snew[j][1];
+      }
+      return true;
+    };
+    const int nplain = min(ntiles, max(0, (vis_all - kb) / kPfKeys));  // tiles with every key visible to every row
+    int it = 0;
+    for (; it < nplain; ++it)
+      if (!iteration(it, std::false_type{})) {
         again = true;
         break;
       }
-      if constexpr (SPAN) {
-        if (it + 3 < ntiles) pf_issue<Sh>(p, trow, k0 + 3 * kPfKeys, ke, h, w, lane, pk_base + (it % 3) * Sh::kPk);
-      }
-      pf_step<HS, KFMT, NT>(r, bufs + (it & 1) * Sh::kBuf, k0, ke, k0 + kPfKeys > vis_all, it == 0, &restart,
-                            pk_next, bufs + ((it + 1) & 1) * Sh::kBuf, k0 + kPfKeys, ke, p.scale_log2, tid, col, g);
-    }
-    wait_vmcnt<0>();
-    __syncthreads();
-    again = again || restart;
+    if (!again)
+      for (; it < ntiles; ++it)
+        if (!iteration(it, std::true_type{})) {
+          again = true;
+          break;
+        }
+    if constexpr (SPAN) wait_vmcnt<0>();
+    __syncthreads();  // no request is written after this point of the pass
+    again = again || restart != kNoRestart;
+    __syncthreads();  // every wave has read the request
+    if (tid == 0) restart = kNoRestart;
     if (!again) break;
-    __syncthreads();  // every wave has seen the flag
-    if (tid == 0) restart = 0;
   }
 
   // ---- epilogue: l over the 4 lane groups, zero-point sum from the extra tile, store
