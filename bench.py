@@ -2,13 +2,19 @@
 
 A step is one split-KV decode + log-sum-exp merge of 2 query tokens (MTP 1) over a 131072-token int4 paged cache,
 24 query / 4 KV heads, head 256, block 16, 8192 shuffled blocks (workload decode-int4-128k-t2): one attention layer
-of one decode step. Inputs are seeded synthetic data resident in HBM before timing.
+of one decode step, launched back to back. Inputs are seeded synthetic data resident in HBM before timing.
 
 Prints one JSON line: decode tok/s (value), HBM GB/s and us per layer, the prefill-chunk workload's tok/s when the
 prefill kernel is available, the roofline of the decode kernel (algorithmic bytes / its average duration measured with
-events on its stream) and the CPU baseline (the dequantise-then-attend restatement timed on this host).
+events on its stream around a run of launches queued behind a spin, so the events see execution only) and the CPU
+baseline (the dequantise-then-attend restatement timed on this host).
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--segments N] [--no-cpu] [--no-prefill]
+    python bench.py --copy-probe MIB     # only a plain device copy of MIB MiB, 10 times (HBM counter calibration)
+
+roofline.traffic is the decode kernel's HBM bytes per launch as the FETCH_SIZE + WRITE_SIZE counters read it, each
+scaled by the ratio of known bytes to counted bytes of the plain copy; the figures come from the committed counter
+summary profiles/decode_span_kernel_decode-int4-128k-t2_traffic.txt (null when it is absent).
 """
 import argparse
 import json
@@ -22,6 +28,8 @@ sys.path.insert(0, os.path.join(HERE, "vllm-quantpack_amd"))
 METRIC = "int4-KV decode tok/s + HBM GB/s at 128k ctx; prefill-chunk tok/s"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+DECODE_KERNEL = "qp::decode_span_kernel<256, 0, 1, 8>"
+SPIN_CYCLES = 50_000_000
 
 
 def log(msg):
@@ -40,28 +48,36 @@ def decode_bench(torch, args):
     sm = torch.empty((T, NQ, S), dtype=torch.float32, device=dev)
     ss = torch.empty((T, NQ, S), dtype=torch.float32, device=dev)
     out = torch.empty((T, NQ, HS), dtype=torch.bfloat16, device=dev)
-    plan = int4_kv.DecodePlan(d["q"], d["k_cache"], d["v_cache"], d["k_scale_cache"], d["v_scale_cache"], out,
-                              cu_seqlens_q=d["cu_seqlens_q"], seqused_k=d["seqused_k"],
-                              block_table=d["block_table"], max_seqlen_q=w.max_query_len,
-                              softmax_scale=w.softmax_scale, num_segments=S, softmax_segm_output=so,
-                              softmax_segm_max=sm, softmax_segm_expsum=ss)
+
+    def make_plan():
+        return int4_kv.DecodePlan(d["q"], d["k_cache"], d["v_cache"], d["k_scale_cache"], d["v_scale_cache"], out,
+                                  cu_seqlens_q=d["cu_seqlens_q"], seqused_k=d["seqused_k"],
+                                  block_table=d["block_table"], max_seqlen_q=w.max_query_len,
+                                  softmax_scale=w.softmax_scale, num_segments=S, softmax_segm_output=so,
+                                  softmax_segm_max=sm, softmax_segm_expsum=ss)
+
+    plan = make_plan()
     for _ in range(args.warmup):
         plan.run()
     torch.cuda.synchronize()
-    # timed region: exactly `steps` steps; decode-kernel events on the launch stream
     stream = torch.cuda.current_stream(dev)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    torch.cuda.synchronize()
+    # timed region: exactly `steps` decode steps (split-KV decode + merge), launched back to back
     t0 = time.perf_counter()
-    for a, b in ev:
-        a.record(stream)
-        plan.decode()
-        b.record(stream)
-        plan.merge()
+    for _ in range(args.steps):
+        plan.run()
     torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    kern_ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
-    step_ms = elapsed * 1e3 / args.steps
+    step_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    # decode-kernel duration: `steps` decode launches queued behind a spin that holds the stream, bracketed by one
+    # pair of events on that stream, so the average is the kernel's execution time in a full queue (an event pair
+    # around every launch would add its own dispatch overhead, about 3 us, to each)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(SPIN_CYCLES)
+    a.record(stream)
+    for _ in range(args.steps):
+        plan.decode()
+    b.record(stream)
+    torch.cuda.synchronize()
+    kern_ms = a.elapsed_time(b) / args.steps
     nbytes = synth.cache_bytes(w)
     result = dict(tokens_per_step=T, step_ms=step_ms, decode_kernel_us=kern_ms * 1e3, bytes=nbytes, segments=S,
                   out=out, w=w)
@@ -69,7 +85,7 @@ def decode_bench(torch, args):
 
 
 def prefill_bench(torch, args):
-    from vllm_quantpack.attention import int4_kv, int4_prefill
+    from vllm_quantpack.attention import int4_prefill
     from vllm_quantpack.tools import synth
     dev = torch.device("cuda:0")
     w = synth.make("prefill-int4-128k-c1024")
@@ -77,7 +93,6 @@ def prefill_bench(torch, args):
     out = torch.empty_like(d["q"])
 
     def step():
-        int4_kv.reshape_and_cache_int4  # noqa: B018  (store is timed separately below)
         int4_prefill.prefill_attention(d["q"], d["k_cache"], d["v_cache"], d["k_scale_cache"], d["v_scale_cache"],
                                        out, cu_seqlens_q=d["cu_seqlens_q"], seqused_k=d["seqused_k"],
                                        block_table=d["block_table"], max_seqlen_q=w.max_query_len,
@@ -102,6 +117,28 @@ def prefill_bench(torch, args):
     cached = n - chunk
     flops = 4.0 * w.head_size * w.num_q_heads * (chunk * cached + chunk * (chunk + 1) / 2)
     return dict(ms=ms, tok_s=chunk / (ms * 1e-3), tflops=flops / (ms * 1e-3) / 1e12, flops=flops)
+
+
+def copy_probe(torch, mib):
+    """A plain device-to-device copy of known size, the calibration kernel for the HBM byte counters."""
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copied {n} bytes 10 times")
+
+
+def counted_traffic():
+    """HBM bytes per decode launch from the committed counter summary, or None."""
+    path = os.path.join(HERE, "profiles", "decode_span_kernel_decode-int4-128k-t2_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch"):
+            return int(line.split("=")[1].split()[0])
+    return None
 
 
 def cpu_baseline(w, budget_s=20.0):
@@ -135,15 +172,19 @@ def main(argv=None):
     ap.add_argument("--segments", type=int, default=0, help="split-KV segments (default: sized for the CU count)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-chunk workload")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB", help="only run a plain copy of MIB MiB")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one MI355X: the int4 KV attention path has no multi-GPU step in this build "
-              "(it shards by KV head with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one MI355X: the int4 KV attention path runs on one GPU here (across GPUs it would "
+              "shard by KV head with no exchange). Run with --gpus 1.", file=sys.stderr)
         return 2
     import torch
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
+    if args.copy_probe:
+        copy_probe(torch, args.copy_probe)
+        return 0
     log(f"device {torch.cuda.get_device_name(0)}, {torch.cuda.get_device_properties(0).multi_processor_count} CUs")
     r = decode_bench(torch, args)
     step_s = r["step_ms"] * 1e-3
@@ -171,7 +212,7 @@ def main(argv=None):
         "hbm_gbps_decode_kernel": round(r["bytes"] / kern_s / 1e9, 1),
         "roofline": {"bound": "hbm", "achieved": round(r["bytes"] / kern_s / 1e9, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(r["bytes"] / kern_s / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "qp::decode_kernel<256,0,1>",
+                     "traffic": counted_traffic(), "kernel": DECODE_KERNEL,
                      "bytes_per_launch": r["bytes"], "avg_us": round(r["decode_kernel_us"], 2)},
     }
     if not args.no_prefill:

@@ -142,6 +142,54 @@ def test_decode_partials_match_the_emulation(device):
     assert O.relerr(go * f[..., None], acc[:, :, :active]) < 1e-2
 
 
+def test_decode_plan_graph_replays(device):
+    """DecodePlan recorded in a HIP graph: three replays, each after eager work that changes the query, each equal
+    to an eager run on the same query and within the fp64 bar."""
+    import torch
+
+    from vllm_quantpack.attention import int4_kv
+    rng = np.random.default_rng(71)
+    T, n, S = 2, 4000, 16
+    nb = -(-n // 16)
+    kv, v = random_cache(rng, nb + 2, NKV, 16, HS, "int4", "hnd")
+    _, (kc, vc, ks, vs) = torch_cache(kv, HS, "int4", device)
+    table = rng.permutation(nb + 2).astype(np.int32)[None, :nb]
+    cu, used, tab = i32([0, T], device), i32([n], device), i32(table, device)
+    q = torch.empty((T, NQ, HS), dtype=torch.bfloat16, device=device)
+    so = torch.empty((T, NQ, S, HS), dtype=torch.float32, device=device)
+    sm = torch.empty((T, NQ, S), dtype=torch.float32, device=device)
+    ss = torch.empty((T, NQ, S), dtype=torch.float32, device=device)
+    out = torch.empty((T, NQ, HS), dtype=torch.bfloat16, device=device)
+    kw = dict(cu_seqlens_q=cu, seqused_k=used, block_table=tab, max_seqlen_q=T, softmax_scale=HS ** -0.5,
+              num_segments=S, softmax_segm_output=so, softmax_segm_max=sm, softmax_segm_expsum=ss)
+    eager = int4_kv.DecodePlan(q, kc, vc, ks, vs, out, **kw)
+    queries = [O.f32_to_bf16_bits(rng.standard_normal((T, NQ, HS)).astype(np.float32)) for _ in range(4)]
+    q.copy_(bf16_tensor(queries[0], device))
+    eager.run()                                        # warm up on the capture-free path first
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            captured = int4_kv.DecodePlan(q, kc, vc, ks, vs, out, **kw)   # launches on the capture stream
+            captured.run()
+    torch.cuda.synchronize()
+    for qb in queries[1:]:
+        q.copy_(bf16_tensor(qb, device))
+        eager.run()
+        torch.cuda.synchronize()
+        want = to_f32(out).copy()
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = to_f32(out)
+        assert np.array_equal(got, want)
+        K, V = O.dequant_f64(v, table[0], n)
+        assert O.relerr(got, O.attention_f64(O.bf16_bits_to_f32(qb), K, V, n, HS ** -0.5)) < 5e-3
+
+
 def test_decode_gqa_8_and_head_128(device):
     rng = np.random.default_rng(51)
     out, emu, ref, _ = _decode_case(device, rng, "int4", [(4, 2500), (1, 700)], nq=16, nkv=2, hs=128, segments=9)
