@@ -2,7 +2,9 @@
 
 A step is one split-KV decode + log-sum-exp merge of 2 query tokens (MTP 1) over a 131072-token int4 paged cache,
 24 query / 4 KV heads, head 256, block 16, 8192 shuffled blocks (workload decode-int4-128k-t2): one attention layer
-of one decode step, launched back to back. Inputs are seeded synthetic data resident in HBM before timing.
+of one decode step, launched back to back. Inputs are seeded synthetic data resident in HBM before timing; the steps
+cycle through --cache-copies independent copies of the cache (4 x 138 MB by default, more than the 256 MB last-level
+cache), so each step reads its cache from HBM rather than from the last-level cache.
 
 Prints one JSON line: decode tok/s (value), HBM GB/s and us per layer, the prefill-chunk workload's tok/s when the
 prefill kernel is available, the roofline of the decode kernel (algorithmic bytes / its average duration measured with
@@ -41,30 +43,29 @@ def decode_bench(torch, args):
     from vllm_quantpack.tools import synth
     dev = torch.device("cuda:0")
     w = synth.make("decode-int4-128k-t2")
-    d = synth.to_device(w, dev)
+    # Independent copies of the layer's cache, used in turn: together they exceed the 256 MB last-level cache, so
+    # every step streams its cache from HBM as it does in a model whose other layers run in between.
+    copies = [synth.to_device(w, dev) for _ in range(args.cache_copies)]
     S = args.segments or int4_kv.segments_for(torch.cuda.get_device_properties(0).multi_processor_count)
     T, NQ, HS = w.q.shape
     so = torch.empty((T, NQ, S, HS), dtype=torch.float32, device=dev)
     sm = torch.empty((T, NQ, S), dtype=torch.float32, device=dev)
     ss = torch.empty((T, NQ, S), dtype=torch.float32, device=dev)
     out = torch.empty((T, NQ, HS), dtype=torch.bfloat16, device=dev)
-
-    def make_plan():
-        return int4_kv.DecodePlan(d["q"], d["k_cache"], d["v_cache"], d["k_scale_cache"], d["v_scale_cache"], out,
-                                  cu_seqlens_q=d["cu_seqlens_q"], seqused_k=d["seqused_k"],
-                                  block_table=d["block_table"], max_seqlen_q=w.max_query_len,
-                                  softmax_scale=w.softmax_scale, num_segments=S, softmax_segm_output=so,
-                                  softmax_segm_max=sm, softmax_segm_expsum=ss)
-
-    plan = make_plan()
-    for _ in range(args.warmup):
-        plan.run()
+    plans = [int4_kv.DecodePlan(d["q"], d["k_cache"], d["v_cache"], d["k_scale_cache"], d["v_scale_cache"], out,
+                                cu_seqlens_q=d["cu_seqlens_q"], seqused_k=d["seqused_k"],
+                                block_table=d["block_table"], max_seqlen_q=w.max_query_len,
+                                softmax_scale=w.softmax_scale, num_segments=S, softmax_segm_output=so,
+                                softmax_segm_max=sm, softmax_segm_expsum=ss) for d in copies]
+    n = len(plans)
+    for i in range(args.warmup):
+        plans[i % n].run()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
     # timed region: exactly `steps` decode steps (split-KV decode + merge), launched back to back
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        plan.run()
+    for i in range(args.steps):
+        plans[i % n].run()
     torch.cuda.synchronize()
     step_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     # decode-kernel duration: `steps` decode launches queued behind a spin that holds the stream, bracketed by one
@@ -73,8 +74,8 @@ def decode_bench(torch, args):
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda._sleep(SPIN_CYCLES)
     a.record(stream)
-    for _ in range(args.steps):
-        plan.decode()
+    for i in range(args.steps):
+        plans[i % n].decode()
     b.record(stream)
     torch.cuda.synchronize()
     kern_ms = a.elapsed_time(b) / args.steps
@@ -172,6 +173,8 @@ def main(argv=None):
     ap.add_argument("--segments", type=int, default=0, help="split-KV segments (default: sized for the CU count)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-chunk workload")
+    ap.add_argument("--cache-copies", type=int, default=4,
+                    help="copies of the decode cache used in turn (1: the cache stays in the last-level cache)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB", help="only run a plain copy of MIB MiB")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -206,7 +209,7 @@ def main(argv=None):
         "data": "synthetic",
         "config": {"workload": "decode-int4-128k-t2", "context": 131072, "query_tokens": 2, "q_heads": 24,
                    "kv_heads": 4, "head_size": 256, "block_size": 16, "kv_format": "int4_per_token_head",
-                   "segments": r["segments"], "parallelism": "single-gpu"},
+                   "segments": r["segments"], "cache_copies": args.cache_copies, "parallelism": "single-gpu"},
         "us_per_layer": round(r["step_ms"] * 1e3, 2),
         "hbm_gbps_step": round(r["bytes"] / step_s / 1e9, 1),
         "hbm_gbps_decode_kernel": round(r["bytes"] / kern_s / 1e9, 1),

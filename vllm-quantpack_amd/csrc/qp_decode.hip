@@ -54,6 +54,10 @@ struct DecodeParams {
 };
 
 constexpr int kChunk = QP_DECODE_TILE;  // keys per wave iteration: two 16-key sub-tiles
+// The running maximum m of a row is raised only when a score exceeds it by more than this (log2 units), so the
+// accumulators are rescaled a handful of times per segment instead of at every new maximum. P = 2^(s - m) then stays
+// below 2^kLazyRescale; the result does not depend on m beyond fp32 rounding.
+constexpr float kLazyRescale = 8.f;
 
 // --------------------------------------------------------------------------------------- per-wave state
 
@@ -192,7 +196,7 @@ __device__ __forceinline__ void compute_chunk(WaveState<HS, KFMT, NCT> &st, cons
                      fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
     mx = fmaxf(mx, shfl_xor_f(mx, 16));
     mx = fmaxf(mx, shfl_xor_f(mx, 32));
-    if (__any(mx > st.m[ct])) {
+    if (__any(mx > st.m[ct] + kLazyRescale)) {
       const float m_new = fmaxf(st.m[ct], mx);
       const float alpha = st.m[ct] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m[ct] - m_new);
       st.l[ct] *= alpha;
@@ -245,9 +249,103 @@ __device__ __forceinline__ void compute_chunk(WaveState<HS, KFMT, NCT> &st, cons
 
 // ------------------------------------------------------------------------ merge of the waves, partial out
 //
-// smem must hold 2 * WAVES * NCT * 16 floats of statistics plus NCT * 16 rows of (HS + 4) floats, and be free.
+// The waves' (acc, m, l) states of one workgroup become one partial: every wave scales its accumulators to the
+// workgroup maximum and parks them in its own LDS slice, then all threads sum the slices and write the partial rows.
+// Three barriers, no serial rounds: the whole merge runs while the memory system is otherwise idle, at the end of the
+// launch. smem must hold merge_lds_bytes and be free (every wave done with its stages once the first barrier passes).
 template <int HS, int KFMT, int NCT, int WAVES>
 __device__ __forceinline__ void finish_workgroup(WaveState<HS, KFMT, NCT> &st, uint8_t *smem, const DecodeParams &p,
+                                                 int w, int col, int g, int q0, int T, int G, int h, int seg_idx) {
+  constexpr int kORow = HS + 4;           // floats per parked row (padding spreads the rows over the banks)
+  constexpr int kRows = NCT * 16;         // rows per wave slice
+  const int R = T * G;
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    st.l[ct] += shfl_xor_f(st.l[ct], 16);
+    st.l[ct] += shfl_xor_f(st.l[ct], 32);
+    st.c[ct] += shfl_xor_f(st.c[ct], 16);
+    st.c[ct] += shfl_xor_f(st.c[ct], 32);
+  }
+  __syncthreads();
+  float *st_m = reinterpret_cast<float *>(smem);
+  float *st_l = st_m + WAVES * kRows;
+  float *obuf = st_l + WAVES * kRows;     // [WAVES][kRows][kORow]
+  if (g == 0) {
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      st_m[w * kRows + ct * 16 + col] = st.m[ct];
+      st_l[w * kRows + ct * 16 + col] = st.l[ct];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < WAVES; ++ww) M = fmaxf(M, st_m[ww * kRows + ct * 16 + col]);
+    const float f = st.m[ct] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m[ct] - M);
+    const float cr = st.c[ct];
+    float *orow = obuf + (w * kRows + ct * 16 + col) * kORow;
+#pragma unroll
+    for (int b = 0; b < HS / 64; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float4 v;
+        v.x = (st.acc[ct][b * 4 + 0][j] - cr) * f;
+        v.y = (st.acc[ct][b * 4 + 1][j] - cr) * f;
+        v.z = (st.acc[ct][b * 4 + 2][j] - cr) * f;
+        v.w = (st.acc[ct][b * 4 + 3][j] - cr) * f;
+        *reinterpret_cast<float4 *>(orow + 64 * b + 16 * g + 4 * j) = v;
+      }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < R * (HS / 4); idx += WAVES * 64) {
+    const int r = idx / (HS / 4), c4 = idx % (HS / 4);
+    const int ct = r / 16, rr = r % 16;
+    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int ww = 0; ww < WAVES; ++ww) {
+      const float4 v = reinterpret_cast<const float4 *>(obuf + (ww * kRows + ct * 16 + rr) * kORow)[c4];
+      sum.x += v.x;
+      sum.y += v.y;
+      sum.z += v.z;
+      sum.w += v.w;
+    }
+    const int t = r / G, j = r % G;
+    float *dst = p.so + (int64_t)(q0 + t) * p.sos0 + (int64_t)(h * G + j) * p.sos1 + (int64_t)seg_idx * p.sos2;
+    reinterpret_cast<float4 *>(dst)[c4] = sum;
+  }
+  if (w == 0 && g == 0) {
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      const int r = ct * 16 + col;
+      if (r < R) {
+        float M = -INFINITY, L = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < WAVES; ++ww) M = fmaxf(M, st_m[ww * kRows + r]);
+#pragma unroll
+        for (int ww = 0; ww < WAVES; ++ww) {
+          const float mw = st_m[ww * kRows + r];
+          if (mw != -INFINITY) L += st_l[ww * kRows + r] * __builtin_amdgcn_exp2f(mw - M);
+        }
+        const int t = r / G, j = r % G;
+        const int64_t o = (int64_t)(q0 + t) * p.sts0 + (int64_t)(h * G + j) * p.sts1 + seg_idx;
+        p.smax[o] = M;
+        p.ssum[o] = L;
+      }
+    }
+  }
+}
+
+template <int HS, int NCT, int WAVES>
+constexpr int merge_lds_bytes() {
+  return 2 * WAVES * NCT * 16 * 4 + WAVES * NCT * 16 * (HS + 4) * 4;
+}
+
+// The same merge in WAVES serial rounds through one shared row buffer: a small LDS footprint for kernels that keep
+// several workgroups per CU.
+template <int HS, int KFMT, int NCT, int WAVES>
+__device__ __forceinline__ void finish_workgroup_serial(WaveState<HS, KFMT, NCT> &st, uint8_t *smem, const DecodeParams &p,
                                                  int w, int col, int g, int q0, int T, int G, int h, int seg_idx) {
   constexpr int kORow = HS + 4;
   const int R = T * G;
@@ -333,9 +431,9 @@ __device__ __forceinline__ void finish_workgroup(WaveState<HS, KFMT, NCT> &st, u
   }
 }
 
-template <int HS, int NCT, int WAVES>
-constexpr int merge_lds_bytes() {
-  return 2 * WAVES * NCT * 16 * 4 + NCT * 16 * (HS + 4) * 4;
+template <int HS, int NCT>
+constexpr int merge_serial_lds_bytes() {
+  return 2 * 16 * NCT * 16 * 4 + NCT * 16 * (HS + 4) * 4;
 }
 
 // --------------------------------------------------------------- generic strided layout: VGPR-staged loader
@@ -414,8 +512,8 @@ template <int HS, int KFMT, int NCT>
 __global__ __launch_bounds__(256) void decode_rows_kernel(const DecodeParams p) {
   constexpr int kWaves = 4;
   using Sh = RowShape<HS, KFMT>;
-  constexpr int kLds = kWaves * Sh::kStage > merge_lds_bytes<HS, NCT, kWaves>() ? kWaves * Sh::kStage
-                                                                                 : merge_lds_bytes<HS, NCT, kWaves>();
+  constexpr int kLds = kWaves * Sh::kStage > merge_serial_lds_bytes<HS, NCT>() ? kWaves * Sh::kStage
+                                                                                : merge_serial_lds_bytes<HS, NCT>();
   __shared__ __attribute__((aligned(16))) uint8_t smem[kLds];
 
   const int lane = threadIdx.x & 63;
@@ -467,7 +565,7 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(const DecodeParams p) 
     compute_chunk<HS, KFMT, NCT, Sh::kKRow, Sh::kVRow>(st, wl, wl + Sh::kVOff, wl + Sh::kFOff, k0, kend, causal_lim,
                                                        col, g);
   }
-  finish_workgroup<HS, KFMT, NCT, kWaves>(st, smem, p, w, col, g, q0, T, G, h, seg_idx);
+  finish_workgroup_serial<HS, KFMT, NCT, kWaves>(st, smem, p, w, col, g, q0, T, G, h, seg_idx);
 }
 
 // ------------------------------------------------------- HND page spans: HBM -> LDS direct, double-buffered
@@ -504,9 +602,9 @@ __device__ __forceinline__ void issue_span_dma(const DecodeParams &p, const int3
         p.kcodes + (int64_t)bid[hc] * p.ks0 + (int64_t)h * p.ks2 + (int64_t)slot0 * Sh::kCell + 16 * lane;
     uint8_t *dst = stage + hc * Sh::kHalf;
 #pragma unroll
-    for (int i = 0; i < Sh::kFull; ++i) dma16(src + 1024 * i, dst + 1024 * i);
+    for (int i = 0; i < Sh::kFull; ++i) dma16_stream(src + 1024 * i, dst + 1024 * i);
     if constexpr (Sh::kRem != 0) {
-      if (lane < Sh::kRem) dma16(src + 1024 * Sh::kFull, dst + 1024 * Sh::kFull);
+      if (lane < Sh::kRem) dma16_stream(src + 1024 * Sh::kFull, dst + 1024 * Sh::kFull);
     }
   }
 }
