@@ -30,7 +30,8 @@ def hipcc():
 
 
 # Per-source extra flags. The prefill kernel keeps its QK^T MFMA results in VGPRs (its PV accumulators own the AGPRs).
-EXTRA = {"qp_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# The decode kernels take no NaN inputs (masked scores are -inf, never NaN), so their maxima need no quieting.
+EXTRA = {"qp_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "qp_decode.hip": ["-fno-honor-nans"]}
 
 
 def _flags(src):

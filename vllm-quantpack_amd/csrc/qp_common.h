@@ -17,6 +17,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -58,6 +59,26 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t 
 // ------------------------------------------------------------------------------------ wave utilities
 
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+// Reductions over the four 16-lane rows of a wave (lanes l, l ^ 16, l ^ 32, l ^ 48), every lane receiving the result:
+// two row swaps on the VALU (v_permlane16_swap, v_permlane32_swap) instead of LDS permutes. Both halves of each swap
+// combine the same pair of rows, so all four rows end with the identical value.
+__device__ __forceinline__ float rows_max(float v) {
+  const uint32_t b = __float_as_uint(v);
+  const auto h = __builtin_amdgcn_permlane16_swap(b, b, false, false);  // rows (0, 0, 2, 2) and (1, 1, 3, 3)
+  const float m = fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1]));
+  const uint32_t mb = __float_as_uint(m);
+  const auto q = __builtin_amdgcn_permlane32_swap(mb, mb, false, false);  // halves (lo, lo) and (hi, hi)
+  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+__device__ __forceinline__ float rows_sum(float v) {
+  const uint32_t b = __float_as_uint(v);
+  const auto h = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+  const float s = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+  const uint32_t sb = __float_as_uint(s);
+  const auto q = __builtin_amdgcn_permlane32_swap(sb, sb, false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
@@ -183,6 +204,16 @@ __device__ __forceinline__ float2 key_floats(uint32_t word, bool is_value, bool 
   } else {
     return make_float2(__uint_as_float(word) * scale_log2, 0.f);
   }
+}
+
+// The value-half scalars in the decode layout: (s_v, zero-point pair) where the pair holds 128 + zp of this key and
+// of the next one as two bf16 integers (0x4300 | zp each), for a bf16 dot with two rounded P * s_v. Lane i takes the
+// next key's word from lane i + 1 of its 16-lane row (DPP row shift), so the pair is only meaningful for even keys
+// with the next key in the same row; s_v is 0 for keys at or past kend.
+__device__ __forceinline__ float2 value_floats_paired(uint32_t word, bool ok) {
+  const uint32_t next = (uint32_t)__builtin_amdgcn_mov_dpp((int)word, 0x101, 0xF, 0xF, false);  // row_shl:1
+  const uint32_t pair = 0x43004300u | (word & 0xFu) | ((next & 0xFu) << 16);
+  return make_float2(ok ? __uint_as_float(word & 0xFFFFFFF0u) : 0.f, __uint_as_float(pair));
 }
 
 // One dwordx4 per lane straight from HBM into LDS at dst + 16 * lane (global_load_lds_dwordx4, LDS base in M0).

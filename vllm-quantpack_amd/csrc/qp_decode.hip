@@ -101,10 +101,7 @@ __device__ __forceinline__ void init_state(WaveState<HS, KFMT, NCT> &st, const D
         st.qop[ct][mi] = as_bf16x8(x);
       }
     }
-    if constexpr (KFMT == QP_CODES_INT4) {
-      qs += shfl_xor_f(qs, 16);
-      qs += shfl_xor_f(qs, 32);
-    }
+    if constexpr (KFMT == QP_CODES_INT4) qs = rows_sum(qs);
     st.qsum[ct] = qs;
     st.m[ct] = -INFINITY;
     st.l[ct] = 0.f;
@@ -116,15 +113,24 @@ __device__ __forceinline__ void init_state(WaveState<HS, KFMT, NCT> &st, const D
 
 // ------------------------------------------------------------------------------------- one 32-key chunk
 //
-// kb/vb: LDS rows of the chunk's 32 keys (key kk at kb + kk * KSTR, vb + kk * VSTR); fb: float4 per key.
+// A chunk runs in two parts. chunk_reads does everything that reads the chunk's LDS rows: S^T = K Q^T on the MFMAs
+// and the fetch of the lane's V codes into registers (ChunkState). chunk_finish then needs only registers and the
+// per-key scalars, so the LDS rows can be refilled with the next chunk while it runs.
+template <int HS, int NCT>
+struct ChunkState {
+  f32x4_t sacc[NCT][2];     // S^T of the two 16-key sub-tiles
+  uint32_t vx[HS / 64][4];  // V codes: [channel block b][key pair d], two keys x four channels (nibbles) each
+};
+
+// kb/vb: LDS rows of the chunk's 32 keys (key kk at kb + kk * KSTR, vb + kk * VSTR).
 template <int HS, int KFMT, int NCT, int KSTR, int VSTR>
-__device__ __forceinline__ void compute_chunk(WaveState<HS, KFMT, NCT> &st, const uint8_t *kb, const uint8_t *vb,
-                                              const uint8_t *fb, int k0, int kend, int causal_lim, int col, int g) {
+__device__ __forceinline__ void chunk_reads(const WaveState<HS, KFMT, NCT> &st, ChunkState<HS, NCT> &cr,
+                                            const uint8_t *kb, const uint8_t *vb, int col, int g) {
   constexpr int kKeyBytes = KFMT == QP_CODES_INT4 ? HS / 2 : HS;
   constexpr int kNmi = HS / 32, kNb = HS / 64;
+  f32x4_t (&sacc)[NCT][2] = cr.sacc;
 
   // ---- S^T = K Q^T, two 16-key sub-tiles
-  f32x4_t sacc[NCT][2];
 #pragma unroll
   for (int sub = 0; sub < 2; ++sub) {
     const uint8_t *kr = kb + (sub * 16 + col) * KSTR + (kKeyBytes / 4) * g;
@@ -162,6 +168,27 @@ __device__ __forceinline__ void compute_chunk(WaveState<HS, KFMT, NCT> &st, cons
     }
   }
 
+  // ---- V codes of the lane: channel quad col + 16 b of keys ka, ka + 1 (16-bit pieces), for every block b
+#pragma unroll
+  for (int b = 0; b < kNb; ++b)
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const int ka = (d < 2 ? 4 * g + 2 * d : 16 + 4 * g + 2 * (d - 2));
+      const uint8_t *vr = vb + 2 * (col + 16 * b);
+      u16x2_t pr;
+      pr[0] = *reinterpret_cast<const uint16_t *>(vr + ka * VSTR);
+      pr[1] = *reinterpret_cast<const uint16_t *>(vr + (ka + 1) * VSTR);
+      cr.vx[b][d] = __builtin_bit_cast(uint32_t, pr);
+    }
+}
+
+// Softmax of the chunk and O^T += V^T P^T; fb: float4 of per-key scalars per key.
+template <int HS, int KFMT, int NCT>
+__device__ __forceinline__ void chunk_finish(WaveState<HS, KFMT, NCT> &st, const ChunkState<HS, NCT> &cr,
+                                             const uint8_t *fb, int k0, int kend, int causal_lim, int g) {
+  constexpr int kNb = HS / 64;
+  const f32x4_t (&sacc)[NCT][2] = cr.sacc;
+
   // ---- per-key scalars of the lane's 8 keys: 4g + j (sub-tile 0) and 16 + 4g + j (sub-tile 1)
   float4 kf[2][4];
 #pragma unroll
@@ -194,8 +221,7 @@ __device__ __forceinline__ void compute_chunk(WaveState<HS, KFMT, NCT> &st, cons
     }
     float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
                      fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
-    mx = fmaxf(mx, shfl_xor_f(mx, 16));
-    mx = fmaxf(mx, shfl_xor_f(mx, 32));
+    mx = rows_max(mx);
     if (__any(mx > st.m[ct] + kLazyRescale)) {
       const float m_new = fmaxf(st.m[ct], mx);
       const float alpha = st.m[ct] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m[ct] - m_new);
@@ -214,8 +240,10 @@ __device__ __forceinline__ void compute_chunk(WaveState<HS, KFMT, NCT> &st, cons
       const float p1 = __builtin_amdgcn_exp2f(s[sub][j0 + 1] - mu);
       lsum += p0 + p1;
       const uint32_t pk = pack_bf16x2(p0 * kf[sub][j0].z, p1 * kf[sub][j0 + 1].z);
-      csum = fmaf(bf16_lo(pk), kf[sub][j0].w, csum);
-      csum = fmaf(bf16_hi(pk), kf[sub][j0 + 1].w, csum);
+      // sum of P16 (128 + zp_v) over the key pair, from the same rounded P16 the MFMA takes
+      csum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk),
+                                             __builtin_bit_cast(bf16x2_t, __float_as_uint(kf[sub][j0].w)), csum,
+                                             false);
       pop[ct][d] = pk;
     }
     st.l[ct] += lsum;
@@ -225,26 +253,26 @@ __device__ __forceinline__ void compute_chunk(WaveState<HS, KFMT, NCT> &st, cons
   // ---- O^T += V^T P^T
 #pragma unroll
   for (int b = 0; b < kNb; ++b) {
-    uint32_t x[4];
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const int ka = (d < 2 ? 4 * g + 2 * d : 16 + 4 * g + 2 * (d - 2));
-      const uint8_t *vr = vb + 2 * (col + 16 * b);
-      const uint32_t lo = *reinterpret_cast<const uint16_t *>(vr + ka * VSTR);
-      const uint32_t hi = *reinterpret_cast<const uint16_t *>(vr + (ka + 1) * VSTR);
-      x[d] = lo | (hi << 16);
-    }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       u32x4_t vv;
 #pragma unroll
-      for (int d = 0; d < 4; ++d) vv[d] = nib_pair(x[d] >> (4 * c));
+      for (int d = 0; d < 4; ++d) vv[d] = nib_pair(cr.vx[b][d] >> (4 * c));
       const bf16x8_t vop = as_bf16x8(vv);
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct)
         st.acc[ct][b * 4 + c] = mfma16x16x32(vop, as_bf16x8(pop[ct]), st.acc[ct][b * 4 + c]);
     }
   }
+}
+
+// Both parts back to back, for loaders whose LDS rows are not refilled during the chunk.
+template <int HS, int KFMT, int NCT, int KSTR, int VSTR>
+__device__ __forceinline__ void compute_chunk(WaveState<HS, KFMT, NCT> &st, const uint8_t *kb, const uint8_t *vb,
+                                              const uint8_t *fb, int k0, int kend, int causal_lim, int col, int g) {
+  ChunkState<HS, NCT> cr;
+  chunk_reads<HS, KFMT, NCT, KSTR, VSTR>(st, cr, kb, vb, col, g);
+  chunk_finish<HS, KFMT, NCT>(st, cr, fb, k0, kend, causal_lim, g);
 }
 
 // ------------------------------------------------------------------------ merge of the waves, partial out
@@ -261,10 +289,8 @@ __device__ __forceinline__ void finish_workgroup(WaveState<HS, KFMT, NCT> &st, u
   const int R = T * G;
 #pragma unroll
   for (int ct = 0; ct < NCT; ++ct) {
-    st.l[ct] += shfl_xor_f(st.l[ct], 16);
-    st.l[ct] += shfl_xor_f(st.l[ct], 32);
-    st.c[ct] += shfl_xor_f(st.c[ct], 16);
-    st.c[ct] += shfl_xor_f(st.c[ct], 32);
+    st.l[ct] = rows_sum(st.l[ct]);
+    st.c[ct] = rows_sum(st.c[ct]);
   }
   __syncthreads();
   float *st_m = reinterpret_cast<float *>(smem);
@@ -351,10 +377,8 @@ __device__ __forceinline__ void finish_workgroup_serial(WaveState<HS, KFMT, NCT>
   const int R = T * G;
 #pragma unroll
   for (int ct = 0; ct < NCT; ++ct) {
-    st.l[ct] += shfl_xor_f(st.l[ct], 16);
-    st.l[ct] += shfl_xor_f(st.l[ct], 32);
-    st.c[ct] += shfl_xor_f(st.c[ct], 16);
-    st.c[ct] += shfl_xor_f(st.c[ct], 32);
+    st.l[ct] = rows_sum(st.l[ct]);
+    st.c[ct] = rows_sum(st.c[ct]);
   }
   __syncthreads();
   float *st_m = reinterpret_cast<float *>(smem);
@@ -556,7 +580,8 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(const DecodeParams p) 
     }
     {
       const int kk = lane & 31;
-      const float2 f = key_floats<KFMT>(regs.w, lane >= 32, k0 + kk < kend, p.scale_log2);
+      const float2 f = lane >= 32 ? value_floats_paired(regs.w, k0 + kk < kend)
+                                  : key_floats<KFMT>(regs.w, false, k0 + kk < kend, p.scale_log2);
       *reinterpret_cast<float2 *>(wl + Sh::kFOff + kk * 16 + (lane < 32 ? 0 : 8)) = f;
     }
     wave_sync();
@@ -656,18 +681,20 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
       const int kk = lane & 31;
       const bool is_v = lane >= 32;
       const uint32_t word = *reinterpret_cast<const uint32_t *>(stage + kk * Sh::kCell + (is_v ? kWordV : kWordK));
-      const float2 f = key_floats<KFMT>(word, is_v, k0 + kk < kend, p.scale_log2);
+      const float2 f = is_v ? value_floats_paired(word, k0 + kk < kend)
+                            : key_floats<KFMT>(word, false, k0 + kk < kend, p.scale_log2);
       *reinterpret_cast<float2 *>(reinterpret_cast<uint8_t *>(fl) + kk * 16 + (is_v ? 8 : 0)) = f;
     }
     wave_sync();
-    compute_chunk<HS, KFMT, NCT, Sh::kCell, Sh::kCell>(st, stage, stage + Sh::kKeyBytes + 4,
-                                                       reinterpret_cast<const uint8_t *>(fl), k0, kend, causal_lim,
-                                                       col, g);
+    ChunkState<HS, NCT> cr;
+    chunk_reads<HS, KFMT, NCT, Sh::kCell, Sh::kCell>(st, cr, stage, stage + Sh::kKeyBytes + 4, col, g);
     if (i + 2 < mine) {
+      // the stage's K and V codes are in registers now: refill it before the softmax and PV run
       wait_lgkm0();  // every read of this stage has returned before the DMA may overwrite it
       wave_sync();
       issue_span_dma<Sh>(p, trow, k0 + 2 * WAVES * kChunk, kend, h, lane, stage);
     }
+    chunk_finish<HS, KFMT, NCT>(st, cr, reinterpret_cast<const uint8_t *>(fl), k0, kend, causal_lim, g);
   }
   finish_workgroup<HS, KFMT, NCT, WAVES>(st, smem, p, w, col, g, q0, T, G, h, seg_idx);
 }
@@ -689,17 +716,17 @@ struct MergeParams {
   float out_scale;
 };
 
-// One workgroup of 256 threads per (token, query head). Thread t reads channels 4 (t % (HS/4)) .. +3 of the
-// segments s = t / (HS/4) + k * (256 / (HS/4)), so every segment row is one coalesced float4 sweep and the loads of
-// different segments are independent; the per-segment weights 2^(m_s - M) are computed once into LDS. With signs,
-// the merged row x is rotated back to (x H D) * out_scale by an in-LDS fast Walsh-Hadamard transform.
+// One workgroup of 256 threads per (token, query head). Thread t owns channels 4 (t % (HS/4)) .. +3 of the segments
+// s = t / (HS/4) + k * (256 / (HS/4)) and folds them in with an online log-sum-exp of its own (a running maximum, the
+// accumulator rescaled when it rises), batch by batch: a batch's segment statistics and rows are all requested before
+// any is used, with no separate pass for the global maximum. The threads' states then combine through LDS. With signs, the merged row x is
+// rotated back to (x H D) * out_scale by an in-LDS fast Walsh-Hadamard transform.
 template <bool RHT>
 __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
-  constexpr int kMaxSeg = 2048;
-  __shared__ float wts[kMaxSeg];
-  __shared__ float red[256];
   __shared__ float4 part[256];
+  __shared__ float pm[256], pl[256];
   __shared__ float row[2][1024];
+  __shared__ float stat[2];
   const int tok = blockIdx.x, head = blockIdx.y, t = threadIdx.x;
   int lo = 0, hi = p.num_seqs - 1;
   while (lo < hi) {  // last sequence whose first query token is <= tok
@@ -712,65 +739,81 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
   const int active = seg > 0 ? min(p.num_segments, (n + seg - 1) / seg) : 0;
   const float *mrow = p.smax + (int64_t)tok * p.sts0 + (int64_t)head * p.sts1;
   const float *lrow = p.ssum + (int64_t)tok * p.sts0 + (int64_t)head * p.sts1;
-  // maximum over segments
-  float M = -INFINITY;
-  for (int s = t; s < active; s += 256) M = fmaxf(M, mrow[s]);
-  red[t] = M;
-  __syncthreads();
-  for (int k = 128; k > 0; k >>= 1) {
-    if (t < k) red[t] = fmaxf(red[t], red[t + k]);
-    __syncthreads();
-  }
-  M = red[0];
-  __syncthreads();
-  // weights and L
-  float L = 0.f;
-  for (int s = t; s < active; s += 256) {
-    const float m = mrow[s];
-    const float wgt = (m == -INFINITY || M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - M);
-    wts[s] = wgt;
-    L = fmaf(lrow[s], wgt, L);
-  }
-  red[t] = L;
-  __syncthreads();
-  for (int k = 128; k > 0; k >>= 1) {
-    if (t < k) red[t] += red[t + k];
-    __syncthreads();
-  }
-  L = red[0];
-  // weighted sum of the segment rows
   const int quads = p.head_size / 4;
   const int groups = 256 / quads;
   const int cq = t % quads, sg = t / quads;
+  float sgn[4];  // rotation signs of the channels this thread writes, requested with the segment loads
+  if constexpr (RHT) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) sgn[k] = t + 256 * k < p.head_size ? p.signs[t + 256 * k] * p.out_scale : 0.f;
+  }
+  float mt = -INFINITY, lt = 0.f;
   float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
   if (sg < groups) {
+    // batches of kBatch segments: every load of a batch is issued before any of it is used
+    constexpr int kBatch = 16;
     const float *orow = p.so + (int64_t)tok * p.sos0 + (int64_t)head * p.sos1 + 4 * cq;
-#pragma unroll 4
-    for (int s = sg; s < active; s += groups) {
-      const float wgt = wts[s];
-      const float4 v = *reinterpret_cast<const float4 *>(orow + (int64_t)s * p.sos2);
-      a.x = fmaf(v.x, wgt, a.x);
-      a.y = fmaf(v.y, wgt, a.y);
-      a.z = fmaf(v.z, wgt, a.z);
-      a.w = fmaf(v.w, wgt, a.w);
+    for (int s0 = sg; s0 < active; s0 += kBatch * groups) {
+      float4 v[kBatch];
+      float ms[kBatch], ls[kBatch];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const int s = s0 + k * groups;
+        const bool ok = s < active;
+        v[k] = ok ? *reinterpret_cast<const float4 *>(orow + (int64_t)s * p.sos2) : make_float4(0.f, 0.f, 0.f, 0.f);
+        ms[k] = ok ? mrow[s] : -INFINITY;
+        ls[k] = ok ? lrow[s] : 0.f;
+      }
+      float bm = mt;
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) bm = fmaxf(bm, ms[k]);
+      if (bm == -INFINITY) continue;
+      const float f = mt == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mt - bm);
+      a.x *= f;
+      a.y *= f;
+      a.z *= f;
+      a.w *= f;
+      lt *= f;
+      mt = bm;
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const float wgt = ms[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[k] - mt);
+        a.x = fmaf(v[k].x, wgt, a.x);
+        a.y = fmaf(v[k].y, wgt, a.y);
+        a.z = fmaf(v[k].z, wgt, a.z);
+        a.w = fmaf(v[k].w, wgt, a.w);
+        lt = fmaf(ls[k], wgt, lt);
+      }
     }
   }
   part[t] = a;
+  pm[t] = mt;
+  pl[t] = lt;
   __syncthreads();
-  const float inv = L > 0.f ? 1.f / L : 0.f;
   if (t < quads) {
-    float4 s4 = part[t];
-    for (int k = 1; k < groups; ++k) {
+    float M = -INFINITY;
+    for (int k = 0; k < groups; ++k) M = fmaxf(M, pm[t + k * quads]);
+    float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    float L = 0.f;
+    for (int k = 0; k < groups; ++k) {
+      const float mk = pm[t + k * quads];
+      const float f = mk == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mk - M);
       const float4 o = part[t + k * quads];
-      s4.x += o.x;
-      s4.y += o.y;
-      s4.z += o.z;
-      s4.w += o.w;
+      s4.x = fmaf(o.x, f, s4.x);
+      s4.y = fmaf(o.y, f, s4.y);
+      s4.z = fmaf(o.z, f, s4.z);
+      s4.w = fmaf(o.w, f, s4.w);
+      L = fmaf(pl[t + k * quads], f, L);
     }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
     row[0][4 * t + 0] = s4.x * inv;
     row[0][4 * t + 1] = s4.y * inv;
     row[0][4 * t + 2] = s4.z * inv;
     row[0][4 * t + 3] = s4.w * inv;
+    if (t == 0) {
+      stat[0] = M;
+      stat[1] = L;
+    }
   }
   __syncthreads();
   int cur = 0;
@@ -784,14 +827,20 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
       __syncthreads();
     }
   }
-  for (int c = t; c < p.head_size; c += 256) {
-    float x = row[cur][c];
-    if constexpr (RHT) x *= p.signs[c] * p.out_scale;
-    p.out[(int64_t)tok * p.os0 + (int64_t)head * p.os1 + c] = f32_to_bf16_bits(x);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int c = t + 256 * k;
+    if (c < p.head_size) {
+      float x = row[cur][c];
+      if constexpr (RHT) x *= sgn[k];
+      p.out[(int64_t)tok * p.os0 + (int64_t)head * p.os1 + c] = f32_to_bf16_bits(x);
+    }
   }
-  if (p.lse && t == 0)
+  if (p.lse && t == 0) {
+    const float M = stat[0], L = stat[1];
     p.lse[(int64_t)tok * p.ls0 + (int64_t)head * p.ls1] =
         (M == -INFINITY || L <= 0.f) ? -INFINITY : (M + __log2f(L)) * 0.6931471805599453f;
+  }
 }
 
 }  // namespace qp
