@@ -65,8 +65,8 @@ int qp_unpack_segment(const qp_cache_half *half, int32_t block_size, int32_t num
                       const int64_t out_stride[2], qp_stream_t stream);
 
 /*
- * Split-KV decode over a paged int4 / k8v4 cache for batches whose sequences have 1..QP_DECODE_MAX_QUERY query
- * tokens: one workgroup per (segment, KV head, sequence) holds every query row of the KV head's GQA group, so the
+ * Split-KV decode over a paged int4 / k8v4 cache (head 128, 256 or 512) for batches whose sequences have
+ * 1..QP_DECODE_MAX_QUERY query tokens: one workgroup per (segment, KV head, sequence) holds every query row of the KV head's GQA group, so the
  * cache is read once per step. Writes unnormalised fp32 segment partials; qp_merge_segments finishes.
  * Replaces the generated _launch_packed_attn_qp / _launch_k8v4_qp 3D path and _attn_packed_qp / _attn_k8v4_qp
  * (int4_kv.py:80-146, 212-216), including the zero-point correction on the bf16-rounded P * s_v (int4_kv.py:90-94).
@@ -132,6 +132,8 @@ int qp_merge_segments(const qp_merge_args *args, qp_stream_t stream);
  * When the query blocks alone cannot fill the device, the keys of each block are split over workgroups
  * (num_splits, 0 = chosen for the device) whose fp32 partials go to the caller's workspace and are merged as in
  * qp_merge_segments; without enough workspace an automatic choice falls back to one split.
+ * Head 512, or more than 12 query heads per KV head, runs the split-KV decode kernel over causal query slices of at
+ * most 4 tokens and merges; that path needs the workspace (qp_prefill_workspace_size bytes, 256-byte aligned).
  * With rht_signs the result is rotated back, out = (o H D) * rht_out_scale, as qp_merge_segments does.
  * Replaces prefill_sequence (int4_prefill.py:203-232: unpack to bf16 segments + FlashAttention + LSE merge, with the
  * inverse single_rht of int4_kv.py:329) and the 2D path of the generated Triton kernel (int4_kv.py:113-118).
@@ -152,7 +154,7 @@ typedef struct qp_prefill_args {
   float softmax_scale;
   void *out;                   /* bf16 [num_tokens, num_q_heads, head_size] */
   int64_t out_stride[2];
-  void *workspace;             /* >= qp_prefill_workspace_size bytes, 16-byte aligned; may be NULL */
+  void *workspace;             /* >= qp_prefill_workspace_size bytes, 256-byte aligned; may be NULL for head 128 / 256 */
   int64_t workspace_bytes;
   const float *rht_signs;      /* optional: inverse rotation of the output (needs a contiguous out) */
   float rht_out_scale;

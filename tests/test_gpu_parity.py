@@ -190,6 +190,17 @@ def test_decode_plan_graph_replays(device):
         assert O.relerr(got, O.attention_f64(O.bf16_bits_to_f32(qb), K, V, n, HS ** -0.5)) < 5e-3
 
 
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+@pytest.mark.parametrize("T", [1, 2, 4])
+def test_decode_head_512(device, fmt, T):
+    """Head 512 with 8 query heads per KV head (Gemma 4 global layers: tests/test_int4_kv.py:194-210,
+    tests/test_k8v4_kv.py:208-225); 4 tokens make 32 query rows, two row tiles."""
+    rng = np.random.default_rng(300 + T + (10 if fmt == "int8" else 0))
+    out, emu, ref, _ = _decode_case(device, rng, fmt, [(T, 3000), (1, 900)], nq=16, nkv=2, hs=512, segments=6)
+    assert O.relerr(out, emu) < 1e-2
+    assert O.relerr(out, ref) < 5e-3
+
+
 def test_decode_gqa_8_and_head_128(device):
     rng = np.random.default_rng(51)
     out, emu, ref, _ = _decode_case(device, rng, "int4", [(4, 2500), (1, 700)], nq=16, nkv=2, hs=128, segments=9)
@@ -442,6 +453,24 @@ def test_prefill_varlen_batch(device):
 def test_prefill_block_sizes_and_gqa(device, bs):
     rng = np.random.default_rng(203 + bs)
     out, emu, ref = _prefill_case(device, rng, "int4", [(40, 2000)], bs=bs, nq=16, nkv=2, hs=128)
+    assert O.relerr(out, emu) < 1e-2
+    assert O.relerr(out, ref) < 5e-3
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+def test_prefill_head_512_query_slices(device, fmt):
+    """Head 512 prefills through the split-KV kernel over causal query slices, then the merge (the reference keeps
+    these on its Triton kernel: tests/test_int4_kv.py:194-210, tests/test_k8v4_kv.py:208-225). Ragged batch."""
+    rng = np.random.default_rng(401 + (1 if fmt == "int8" else 0))
+    out, emu, ref = _prefill_case(device, rng, fmt, [(37, 2100), (5, 600), (1, 64)], nq=16, nkv=2, hs=512)
+    assert O.relerr(out, emu) < 1e-2
+    assert O.relerr(out, ref) < 5e-3
+
+
+def test_prefill_wide_gqa_query_slices(device):
+    """16 query heads per KV head is past the MFMA prefill kernel's 12 and takes the slice path as well."""
+    rng = np.random.default_rng(405)
+    out, emu, ref = _prefill_case(device, rng, "int4", [(20, 1500), (3, 200)], nq=16, nkv=1, hs=128)
     assert O.relerr(out, emu) < 1e-2
     assert O.relerr(out, ref) < 5e-3
 

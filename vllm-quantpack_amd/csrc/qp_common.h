@@ -99,6 +99,13 @@ namespace qp {
 void set_error(const std::string &msg);
 int fail(int code, const std::string &msg);
 int launch_status();
+int device_cus();
+
+// Prefill through the split-KV decode kernel over query slices of at most 4 tokens (causal within each sequence),
+// then the log-sum-exp merge: the path for shapes the MFMA prefill kernel does not take (head 512, more than 12
+// query heads per KV head). Arguments and workspace are those of qp_prefill; defined with the decode kernels.
+int64_t slice_prefill_workspace(const qp_paged_cache *cache, const qp_prefill_args *a);
+int slice_prefill(const qp_paged_cache *cache, const qp_prefill_args *a, hipStream_t stream);
 
 // Exact magic division for 0 <= x < 2^31 by d >= 2: m = ceil(2^(31+l) / d), l = ceil(log2 d);
 // x / d == umulhi(x, m) >> (l - 1).

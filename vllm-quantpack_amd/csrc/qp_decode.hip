@@ -51,7 +51,50 @@ struct DecodeParams {
   int32_t num_q_heads, num_kv_heads, block_size, num_segments;
   uint32_t bs_magic, bs_shift;  // pos / block_size == umulhi(pos, bs_magic) >> bs_shift for pos < 2^31
   float scale_log2;             // softmax_scale * log2(e)
+  // Query slices (prefill through the split-KV kernel): when set, workgroup z takes slice z = (sequence, first token
+  // index, token count, context of its last token) instead of sequence z; count 0 = nothing to do.
+  const int4 *slices;
 };
+
+// The work of one workgroup: query tokens [q0, q0 + T) of sequence seq, context n for its last token, keys
+// [kstart, kend) of segment seg_idx. Segments follow the sequence's full context (as the merge does), so in slice mode
+// a segment can lie wholly past the slice's context: its statistics are written as empty (m = -inf, l = 0) for the
+// merge and the workgroup stops.
+struct DecodeWork {
+  int seq, q0, T, n, kstart, kend;
+};
+
+__device__ __forceinline__ bool decode_work(const DecodeParams &p, int G, int h, int seg_idx, DecodeWork &d) {
+  int nfull;
+  if (p.slices) {
+    const int4 sl = p.slices[blockIdx.z];
+    d.seq = sl.x;
+    d.q0 = sl.y;
+    d.T = sl.z;
+    d.n = sl.w;
+    if (d.T <= 0) return false;
+    nfull = p.used_k[d.seq];
+  } else {
+    d.seq = blockIdx.z;
+    d.q0 = p.cu_q[d.seq];
+    d.T = p.cu_q[d.seq + 1] - d.q0;
+    d.n = p.used_k[d.seq];
+    nfull = d.n;
+  }
+  if (d.T <= 0 || nfull <= 0) return false;
+  const int seg = (nfull + p.num_segments * QP_DECODE_TILE - 1) / (p.num_segments * QP_DECODE_TILE) * QP_DECODE_TILE;
+  d.kstart = seg_idx * seg;
+  d.kend = min(d.n, d.kstart + seg);
+  if (d.kstart < d.kend) return true;
+  if (p.slices && d.kstart < nfull) {
+    for (int r = threadIdx.x; r < d.T * G; r += blockDim.x) {
+      const int64_t o = (int64_t)(d.q0 + r / G) * p.sts0 + (int64_t)(h * G + r % G) * p.sts1 + seg_idx;
+      p.smax[o] = -INFINITY;
+      p.ssum[o] = 0.f;
+    }
+  }
+  return false;
+}
 
 constexpr int kChunk = QP_DECODE_TILE;  // keys per wave iteration: two 16-key sub-tiles
 // The running maximum m of a row is raised only when a score exceeds it by more than this (log2 units), so the
@@ -542,16 +585,11 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(const DecodeParams p) 
 
   const int lane = threadIdx.x & 63;
   const int w = uniform(threadIdx.x >> 6);
-  const int seg_idx = blockIdx.x, h = blockIdx.y, seq = blockIdx.z;
-  const int q0 = p.cu_q[seq];
-  const int T = p.cu_q[seq + 1] - q0;
-  const int n = p.used_k[seq];
-  if (T <= 0 || n <= 0) return;
+  const int seg_idx = blockIdx.x, h = blockIdx.y;
   const int G = p.num_q_heads / p.num_kv_heads;
-  const int seg = (n + p.num_segments * kChunk - 1) / (p.num_segments * kChunk) * kChunk;
-  const int kstart = seg_idx * seg;
-  const int kend = min(n, kstart + seg);
-  if (kstart >= kend) return;
+  DecodeWork d;
+  if (!decode_work(p, G, h, seg_idx, d)) return;
+  const int seq = d.seq, q0 = d.q0, T = d.T, n = d.n, kstart = d.kstart, kend = d.kend;
   const int col = lane & 15, g = lane >> 4;
 
   WaveState<HS, KFMT, NCT> st;
@@ -637,9 +675,14 @@ __device__ __forceinline__ void issue_span_dma(const DecodeParams &p, const int3
 template <int HS, int KFMT, int NCT, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodeParams p) {
   using Sh = SpanShape<HS, KFMT>;
-  constexpr int kStages = 2;
+  // two stages per wave where they fit (one for k8v4 keys at head 512), the parallel merge where it fits
+  constexpr int kLdsMax = 160 * 1024 - 4096;
+  constexpr int kStages = WAVES * 2 * 2 * Sh::kHalf + WAVES * 2 * kChunk * 16 <= kLdsMax ? 2 : 1;
   constexpr int kCells = WAVES * kStages * 2 * Sh::kHalf;
-  constexpr int kLds = kCells > merge_lds_bytes<HS, NCT, WAVES>() ? kCells : merge_lds_bytes<HS, NCT, WAVES>();
+  constexpr int kFl = WAVES * kStages * kChunk * 16;
+  constexpr bool kParMerge = merge_lds_bytes<HS, NCT, WAVES>() + kFl <= kLdsMax;
+  constexpr int kMerge = kParMerge ? merge_lds_bytes<HS, NCT, WAVES>() : merge_serial_lds_bytes<HS, NCT>();
+  constexpr int kLds = kCells > kMerge ? kCells : kMerge;
   // cells (DMA destinations) and per-key scalars live in different allocations, so the compiler can tell the
   // scalar stores from the in-flight copies and does not wait for the copies before them
   __shared__ __attribute__((aligned(16))) uint8_t smem[kLds];
@@ -647,16 +690,11 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
 
   const int lane = threadIdx.x & 63;
   const int w = uniform(threadIdx.x >> 6);
-  const int seg_idx = blockIdx.x, h = blockIdx.y, seq = blockIdx.z;
-  const int q0 = p.cu_q[seq];
-  const int T = p.cu_q[seq + 1] - q0;
-  const int n = p.used_k[seq];
-  if (T <= 0 || n <= 0) return;
+  const int seg_idx = blockIdx.x, h = blockIdx.y;
   const int G = p.num_q_heads / p.num_kv_heads;
-  const int seg = (n + p.num_segments * kChunk - 1) / (p.num_segments * kChunk) * kChunk;
-  const int kstart = seg_idx * seg;
-  const int kend = min(n, kstart + seg);
-  if (kstart >= kend) return;
+  DecodeWork d;
+  if (!decode_work(p, G, h, seg_idx, d)) return;
+  const int seq = d.seq, q0 = d.q0, T = d.T, n = d.n, kstart = d.kstart, kend = d.kend;
   const int col = lane & 15, g = lane >> 4;
 
   WaveState<HS, KFMT, NCT> st;
@@ -670,12 +708,13 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
   constexpr int kWordK = Sh::kKeyBytes, kWordV = Sh::kCell - 4;
 
   if (mine > 0) issue_span_dma<Sh>(p, trow, kstart + w * kChunk, kend, h, lane, wl);
-  if (mine > 1) issue_span_dma<Sh>(p, trow, kstart + (w + WAVES) * kChunk, kend, h, lane, wl + 2 * Sh::kHalf);
+  if (kStages > 1 && mine > 1)
+    issue_span_dma<Sh>(p, trow, kstart + (w + WAVES) * kChunk, kend, h, lane, wl + 2 * Sh::kHalf);
   for (int i = 0; i < mine; ++i) {
     const int k0 = kstart + (w + i * WAVES) * kChunk;
-    uint8_t *stage = wl + (i & 1) * 2 * Sh::kHalf;
-    float4 *fl = kfl[w][i & 1];
-    if (i + 1 < mine) wait_vmcnt<Sh::kDmaPerChunk>();
+    uint8_t *stage = wl + (i % kStages) * 2 * Sh::kHalf;
+    float4 *fl = kfl[w][i % kStages];
+    if (kStages > 1 && i + 1 < mine) wait_vmcnt<Sh::kDmaPerChunk>();
     else wait_vmcnt<0>();
     {  // per-key scalars from the words now in LDS
       const int kk = lane & 31;
@@ -688,15 +727,16 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
     wave_sync();
     ChunkState<HS, NCT> cr;
     chunk_reads<HS, KFMT, NCT, Sh::kCell, Sh::kCell>(st, cr, stage, stage + Sh::kKeyBytes + 4, col, g);
-    if (i + 2 < mine) {
+    if (i + kStages < mine) {
       // the stage's K and V codes are in registers now: refill it before the softmax and PV run
       wait_lgkm0();  // every read of this stage has returned before the DMA may overwrite it
       wave_sync();
-      issue_span_dma<Sh>(p, trow, k0 + 2 * WAVES * kChunk, kend, h, lane, stage);
+      issue_span_dma<Sh>(p, trow, k0 + kStages * WAVES * kChunk, kend, h, lane, stage);
     }
     chunk_finish<HS, KFMT, NCT>(st, cr, reinterpret_cast<const uint8_t *>(fl), k0, kend, causal_lim, g);
   }
-  finish_workgroup<HS, KFMT, NCT, WAVES>(st, smem, p, w, col, g, q0, T, G, h, seg_idx);
+  if constexpr (kParMerge) finish_workgroup<HS, KFMT, NCT, WAVES>(st, smem, p, w, col, g, q0, T, G, h, seg_idx);
+  else finish_workgroup_serial<HS, KFMT, NCT, WAVES>(st, smem, p, w, col, g, q0, T, G, h, seg_idx);
 }
 
 // ------------------------------------------------------------------------------------------------- merge
@@ -777,7 +817,8 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
       mt = bm;
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) {
-        const float wgt = ms[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[k] - mt);
+        if (ms[k] == -INFINITY) continue;  // an empty segment: its row was not written
+        const float wgt = __builtin_amdgcn_exp2f(ms[k] - mt);
         a.x = fmaf(v[k].x, wgt, a.x);
         a.y = fmaf(v[k].y, wgt, a.y);
         a.z = fmaf(v[k].z, wgt, a.z);
@@ -843,6 +884,43 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
   }
 }
 
+// Query slices of every sequence for the slice prefill: tokens [t0, t0 + ts) of sequence i (the last one shorter),
+// each with the context of its last token, listed sequence by sequence; unused entries of the table get count 0.
+__global__ __launch_bounds__(256) void build_slices_kernel(const int32_t *cu_q, const int32_t *used_k, int num_seqs,
+                                                           int ts, int max_slices, int4 *slices) {
+  __shared__ int off[257];
+  int base = 0;
+  for (int s0 = 0; s0 < num_seqs; s0 += 256) {
+    const int i = s0 + (int)threadIdx.x;
+    int cnt = 0, T = 0, n = 0, q0 = 0;
+    if (i < num_seqs) {
+      q0 = cu_q[i];
+      T = cu_q[i + 1] - q0;
+      n = used_k[i];
+      cnt = T > 0 ? (T + ts - 1) / ts : 0;
+    }
+    off[threadIdx.x] = cnt;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int acc = base;
+      for (int k = 0; k < 256; ++k) {
+        const int c = off[k];
+        off[k] = acc;
+        acc += c;
+      }
+      off[256] = acc;
+    }
+    __syncthreads();
+    for (int j = 0; j < cnt; ++j) {
+      const int t0 = j * ts, tj = min(ts, T - t0), k = off[threadIdx.x] + j;
+      if (k < max_slices) slices[k] = make_int4(i, q0 + t0, tj, n - T + t0 + tj);
+    }
+    base = off[256];
+    __syncthreads();
+  }
+  for (int k = base + (int)threadIdx.x; k < max_slices; k += 256) slices[k] = make_int4(0, 0, 0, 0);
+}
+
 }  // namespace qp
 
 using namespace qp;
@@ -852,13 +930,40 @@ namespace {
 template <int HS, int KFMT, int NCT>
 void launch_decode(const DecodeParams &p, dim3 grid, bool span, hipStream_t s) {
   if (span) {
-    // 8 waves (2 per SIMD) fit the registers of one row tile with int4 keys; the others run 4.
-    constexpr int kWaves = (KFMT == QP_CODES_INT4 && NCT == 1) ? 8 : 4;
+    // 8 waves (2 per SIMD) fit the registers of one row tile with int4 keys up to head 256; the others run 4.
+    constexpr int kWaves = (KFMT == QP_CODES_INT4 && NCT == 1 && HS <= 256) ? 8 : 4;
     decode_span_kernel<HS, KFMT, NCT, kWaves><<<grid, kWaves * 64, 0, s>>>(p);
+  } else if constexpr (HS == 512 && KFMT == QP_CODES_INT8) {
+    set_error("qp_decode_splitkv: head 512 with int8 keys needs the standard cell layout");
   } else {
     decode_rows_kernel<HS, KFMT, NCT><<<grid, 256, 0, s>>>(p);
   }
 }
+
+// The cache views, block-size division and KV head count of DecodeParams.
+void cache_params(const qp_paged_cache *cache, DecodeParams &p) {
+  p.kcodes = static_cast<const uint8_t *>(cache->key.codes);
+  p.ks0 = cache->key.code_stride[0];
+  p.ks1 = cache->key.code_stride[1];
+  p.ks2 = cache->key.code_stride[2];
+  p.vcodes = static_cast<const uint8_t *>(cache->value.codes);
+  p.vs0 = cache->value.code_stride[0];
+  p.vs1 = cache->value.code_stride[1];
+  p.vs2 = cache->value.code_stride[2];
+  p.kwords = static_cast<const uint32_t *>(cache->key.words);
+  p.kws0 = cache->key.word_stride[0];
+  p.kws1 = cache->key.word_stride[1];
+  p.kws2 = cache->key.word_stride[2];
+  p.vwords = static_cast<const uint32_t *>(cache->value.words);
+  p.vws0 = cache->value.word_stride[0];
+  p.vws1 = cache->value.word_stride[1];
+  p.vws2 = cache->value.word_stride[2];
+  p.num_kv_heads = cache->num_kv_heads;
+  p.block_size = cache->block_size;
+  div_magic((uint32_t)cache->block_size, &p.bs_magic, &p.bs_shift);
+}
+
+int dispatch_hs(const qp_paged_cache *cache, const DecodeParams &p, int nct, dim3 grid, hipStream_t s);
 
 template <int HS>
 int dispatch_decode(const DecodeParams &p, int kfmt, int nct, dim3 grid, bool span, hipStream_t s) {
@@ -882,7 +987,7 @@ extern "C" int qp_decode_splitkv(const qp_paged_cache *cache, const qp_decode_ar
                  a->segm_expsum,
              "qp_decode_splitkv: null tensor");
   const int hs = cache->head_size;
-  QP_SUPPORTED(hs == 128 || hs == 256, "qp_decode_splitkv: head size must be 128 or 256");
+  QP_SUPPORTED(hs == 128 || hs == 256 || hs == 512, "qp_decode_splitkv: head size must be 128, 256 or 512");
   QP_REQUIRE(cache->key.format == QP_CODES_INT4 || cache->key.format == QP_CODES_INT8,
              "qp_decode_splitkv: unknown key format");
   QP_REQUIRE(cache->value.format == QP_CODES_INT4, "qp_decode_splitkv: values must be int4");
@@ -915,22 +1020,7 @@ extern "C" int qp_decode_splitkv(const qp_paged_cache *cache, const qp_decode_ar
   if (a->num_seqs == 0 || a->num_tokens == 0) return QP_OK;
 
   DecodeParams p;
-  p.kcodes = static_cast<const uint8_t *>(cache->key.codes);
-  p.ks0 = cache->key.code_stride[0];
-  p.ks1 = cache->key.code_stride[1];
-  p.ks2 = cache->key.code_stride[2];
-  p.vcodes = static_cast<const uint8_t *>(cache->value.codes);
-  p.vs0 = cache->value.code_stride[0];
-  p.vs1 = cache->value.code_stride[1];
-  p.vs2 = cache->value.code_stride[2];
-  p.kwords = static_cast<const uint32_t *>(cache->key.words);
-  p.kws0 = cache->key.word_stride[0];
-  p.kws1 = cache->key.word_stride[1];
-  p.kws2 = cache->key.word_stride[2];
-  p.vwords = static_cast<const uint32_t *>(cache->value.words);
-  p.vws0 = cache->value.word_stride[0];
-  p.vws1 = cache->value.word_stride[1];
-  p.vws2 = cache->value.word_stride[2];
+  cache_params(cache, p);
   p.q = static_cast<const uint16_t *>(a->query);
   p.qs0 = a->query_stride[0];
   p.qs1 = a->query_stride[1];
@@ -947,17 +1037,13 @@ extern "C" int qp_decode_splitkv(const qp_paged_cache *cache, const qp_decode_ar
   p.sts0 = a->segm_stat_stride[0];
   p.sts1 = a->segm_stat_stride[1];
   p.num_q_heads = a->num_q_heads;
-  p.num_kv_heads = cache->num_kv_heads;
-  p.block_size = cache->block_size;
   p.num_segments = a->num_segments;
-  div_magic((uint32_t)cache->block_size, &p.bs_magic, &p.bs_shift);
   p.scale_log2 = a->softmax_scale * kLog2e;
+  p.slices = nullptr;
   const int nct = rows > 16 ? 2 : 1;
-  const bool span = is_span_layout(cache) && !getenv("QP_DECODE_ROWS");
   const dim3 grid(a->num_segments, cache->num_kv_heads, a->num_seqs);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (hs == 256) return dispatch_decode<256>(p, cache->key.format, nct, grid, span, s);
-  return dispatch_decode<128>(p, cache->key.format, nct, grid, span, s);
+  return dispatch_hs(cache, p, nct, grid, s);
 }
 
 extern "C" int qp_merge_segments(const qp_merge_args *a, qp_stream_t stream) {
@@ -1000,3 +1086,118 @@ extern "C" int qp_merge_segments(const qp_merge_args *a, qp_stream_t stream) {
   else merge_kernel<false><<<grid, 256, 0, s>>>(p);
   return launch_status();
 }
+
+namespace {
+
+int dispatch_hs(const qp_paged_cache *cache, const DecodeParams &p, int nct, dim3 grid, hipStream_t s) {
+  const int hs = cache->head_size;
+  const bool span = is_span_layout(cache) && !getenv("QP_DECODE_ROWS");
+  QP_SUPPORTED(span || hs != 512 || cache->key.format == QP_CODES_INT4,
+               "head 512 with int8 keys needs the standard cell layout");
+  if (hs == 512) return dispatch_decode<512>(p, cache->key.format, nct, grid, span, s);
+  if (hs == 256) return dispatch_decode<256>(p, cache->key.format, nct, grid, span, s);
+  return dispatch_decode<128>(p, cache->key.format, nct, grid, span, s);
+}
+
+// Slice prefill geometry: ts query tokens per slice (at most 16 query rows, so one row tile), S key segments per
+// slice, and the workspace carve-up [slice table | segment rows | segment max | segment sum].
+struct SliceLayout {
+  int ts, segments, max_slices;
+  int64_t off_rows, off_max, off_sum, total;
+};
+
+SliceLayout slice_layout(const qp_paged_cache *cache, const qp_prefill_args *a) {
+  SliceLayout L;
+  const int G = a->num_q_heads / cache->num_kv_heads;
+  L.ts = G >= 16 ? 1 : (16 / G < QP_DECODE_MAX_QUERY ? 16 / G : QP_DECODE_MAX_QUERY);
+  L.max_slices = a->num_tokens / L.ts + a->num_seqs;
+  const int64_t est = ((int64_t)a->num_tokens + L.ts - 1) / L.ts;
+  const int64_t want = (2 * (int64_t)device_cus() + est * cache->num_kv_heads - 1) / (est * cache->num_kv_heads);
+  int S = (int)(want < 1 ? 1 : (want > 64 ? 64 : want));
+  const int by_len = a->max_seqlen_k > 0 ? a->max_seqlen_k / 256 : 64;
+  if (S > by_len) S = by_len < 1 ? 1 : by_len;
+  L.segments = S;
+  auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
+  const int64_t rows = (int64_t)a->num_tokens * a->num_q_heads * S;
+  L.off_rows = up((int64_t)L.max_slices * 16);
+  L.off_max = L.off_rows + up(rows * cache->head_size * 4);
+  L.off_sum = L.off_max + up(rows * 4);
+  L.total = L.off_sum + up(rows * 4);
+  return L;
+}
+
+}  // namespace
+
+namespace qp {
+
+int64_t slice_prefill_workspace(const qp_paged_cache *cache, const qp_prefill_args *a) {
+  return slice_layout(cache, a).total;
+}
+
+int slice_prefill(const qp_paged_cache *cache, const qp_prefill_args *a, hipStream_t s) {
+  const int hs = cache->head_size;
+  const int G = a->num_q_heads / cache->num_kv_heads;
+  QP_SUPPORTED(G <= 32, "qp_prefill: at most 32 query heads per KV head");
+  if (a->num_seqs == 0 || a->num_tokens == 0) return QP_OK;
+  const SliceLayout L = slice_layout(cache, a);
+  QP_REQUIRE(a->workspace && a->workspace_bytes >= L.total && aligned(a->workspace, 256),
+             "qp_prefill: this shape needs a 256-byte aligned workspace of qp_prefill_workspace_size bytes");
+  uint8_t *ws = static_cast<uint8_t *>(a->workspace);
+  int4 *slices = reinterpret_cast<int4 *>(ws);
+  float *so = reinterpret_cast<float *>(ws + L.off_rows);
+  float *sm = reinterpret_cast<float *>(ws + L.off_max);
+  float *ss = reinterpret_cast<float *>(ws + L.off_sum);
+  build_slices_kernel<<<1, 256, 0, s>>>(a->cu_seqlens_q, a->seqused_k, a->num_seqs, L.ts, L.max_slices, slices);
+  int st = launch_status();
+  if (st != QP_OK) return st;
+
+  DecodeParams p;
+  cache_params(cache, p);
+  p.q = static_cast<const uint16_t *>(a->query);
+  p.qs0 = a->query_stride[0];
+  p.qs1 = a->query_stride[1];
+  p.cu_q = a->cu_seqlens_q;
+  p.used_k = a->seqused_k;
+  p.table = a->block_table;
+  p.table_stride = a->block_table_stride;
+  p.so = so;
+  p.sos2 = hs;
+  p.sos1 = (int64_t)L.segments * hs;
+  p.sos0 = (int64_t)a->num_q_heads * p.sos1;
+  p.smax = sm;
+  p.ssum = ss;
+  p.sts1 = L.segments;
+  p.sts0 = (int64_t)a->num_q_heads * L.segments;
+  p.num_q_heads = a->num_q_heads;
+  p.num_segments = L.segments;
+  p.scale_log2 = a->softmax_scale * kLog2e;
+  p.slices = slices;
+  const int nct = L.ts * G > 16 ? 2 : 1;
+  st = dispatch_hs(cache, p, nct, dim3(L.segments, cache->num_kv_heads, L.max_slices), s);
+  if (st != QP_OK) return st;
+
+  qp_merge_args m = {};
+  m.segm_output = so;
+  m.segm_output_stride[0] = p.sos0;
+  m.segm_output_stride[1] = p.sos1;
+  m.segm_output_stride[2] = hs;
+  m.segm_max = sm;
+  m.segm_expsum = ss;
+  m.segm_stat_stride[0] = p.sts0;
+  m.segm_stat_stride[1] = p.sts1;
+  m.cu_seqlens_q = a->cu_seqlens_q;
+  m.seqused_k = a->seqused_k;
+  m.num_seqs = a->num_seqs;
+  m.num_tokens = a->num_tokens;
+  m.num_q_heads = a->num_q_heads;
+  m.head_size = hs;
+  m.num_segments = L.segments;
+  m.out = a->out;
+  m.out_stride[0] = a->out_stride[0];
+  m.out_stride[1] = a->out_stride[1];
+  m.rht_signs = a->rht_signs;
+  m.rht_out_scale = a->rht_out_scale;
+  return qp_merge_segments(&m, reinterpret_cast<qp_stream_t>(s));
+}
+
+}  // namespace qp

@@ -790,18 +790,6 @@ void prefill_geometry(int G, int max_query_len, int *nt, int *bq) {
   *bq = 16 * k;
 }
 
-int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cached[dev] = cus;
-  }
-  return cached[dev];
-}
-
 // Key splits per query block: enough workgroups for one per CU, each split keeping >= 1024 keys.
 int prefill_splits(const qp_paged_cache *cache, const qp_prefill_args *a, int bq) {
   if (a->num_splits > 0) return a->num_splits;
@@ -835,10 +823,15 @@ void dispatch_nt(const PrefillParams &p, int nt, dim3 grid, bool span, hipStream
 
 }  // namespace
 
+// Shapes the MFMA prefill kernel takes: head 128 or 256, at most 12 query heads per KV head.
+static bool mfma_prefill_shape(const qp_paged_cache *cache, const qp_prefill_args *a) {
+  return (cache->head_size == 128 || cache->head_size == 256) && a->num_q_heads / cache->num_kv_heads <= 12;
+}
+
 extern "C" int64_t qp_prefill_workspace_size(const qp_paged_cache *cache, const qp_prefill_args *a) {
-  if (!cache || !a || cache->num_kv_heads <= 0 || a->num_q_heads <= 0 || a->num_q_heads % cache->num_kv_heads ||
-      a->num_q_heads / cache->num_kv_heads > 12)
+  if (!cache || !a || cache->num_kv_heads <= 0 || a->num_q_heads <= 0 || a->num_q_heads % cache->num_kv_heads)
     return 0;
+  if (!mfma_prefill_shape(cache, a)) return slice_prefill_workspace(cache, a);
   int nt, bq;
   prefill_geometry(a->num_q_heads / cache->num_kv_heads, a->max_query_len, &nt, &bq);
   return partial_bytes(cache, a, prefill_splits(cache, a, bq));
@@ -850,13 +843,12 @@ extern "C" int qp_prefill(const qp_paged_cache *cache, const qp_prefill_args *a,
              "qp_prefill: null cache view");
   QP_REQUIRE(a->query && a->cu_seqlens_q && a->seqused_k && a->block_table && a->out, "qp_prefill: null tensor");
   const int hs = cache->head_size;
-  QP_SUPPORTED(hs == 128 || hs == 256, "qp_prefill: head size must be 128 or 256");
+  QP_SUPPORTED(hs == 128 || hs == 256 || hs == 512, "qp_prefill: head size must be 128, 256 or 512");
   QP_REQUIRE(cache->key.format == QP_CODES_INT4 || cache->key.format == QP_CODES_INT8, "qp_prefill: bad key format");
   QP_REQUIRE(cache->value.format == QP_CODES_INT4, "qp_prefill: values must be int4");
   QP_REQUIRE(cache->num_kv_heads > 0 && a->num_q_heads > 0 && a->num_q_heads % cache->num_kv_heads == 0,
              "qp_prefill: query heads must be a multiple of KV heads");
   const int G = a->num_q_heads / cache->num_kv_heads;
-  QP_SUPPORTED(G <= 12, "qp_prefill: at most 12 query heads per KV head");
   QP_SUPPORTED(cache->block_size >= 16 && cache->block_size % 16 == 0,
                "qp_prefill: block size must be a multiple of 16");
   QP_REQUIRE(a->num_seqs >= 0 && a->num_tokens >= 0 && a->max_query_len >= 0 && a->max_seqlen_k >= 0,
@@ -875,6 +867,7 @@ extern "C" int qp_prefill(const qp_paged_cache *cache, const qp_prefill_args *a,
   QP_REQUIRE(!a->rht_signs || (a->out_stride[1] == hs && a->out_stride[0] == (int64_t)a->num_q_heads * hs),
              "qp_prefill: the output rotation needs a contiguous output");
   if (a->num_seqs == 0 || a->num_tokens == 0) return QP_OK;
+  if (!mfma_prefill_shape(cache, a)) return slice_prefill(cache, a, reinterpret_cast<hipStream_t>(stream));
   int nt, bq;
   prefill_geometry(G, a->max_query_len, &nt, &bq);
   int splits = prefill_splits(cache, a, bq);

@@ -117,7 +117,7 @@ def unified_attention_int4(q, k_cache, v_cache, out, *, cu_seqlens_q, max_seqlen
     rows = int(max_seqlen_q) * (q.shape[1] // nkv)
     decode = (int(max_seqlen_q) <= MAX_Q_SPLIT_KV and rows <= MAX_DECODE_ROWS and softmax_segm_output is not None
               and q.shape[0] <= softmax_segm_output.shape[0] and num_par_softmax_segments
-              and hs in (128, 256))
+              and hs in (128, 256, 512))
     if decode:
         target = out if (out.dtype == torch.bfloat16 and out.stride(-1) == 1) else torch.empty_like(q)
         paged_decode(q_rot, k_cache, v_cache, k_scale_cache, v_scale_cache, target, cu_seqlens_q=cu_seqlens_q,

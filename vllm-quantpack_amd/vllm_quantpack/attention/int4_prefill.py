@@ -13,7 +13,7 @@ import torch
 
 from .. import _hip
 
-MAX_HEAD = 256       # largest head size of the MFMA prefill kernel
+MAX_HEAD = 256       # largest head size of the MFMA prefill kernel (head 512 prefills through split-KV query slices)
 SEGMENT = 16384      # the reference's unpack segment; kept for callers that size bf16 scratch the same way
 MIN_QUERY = 64       # chunks at least this long take the prefill kernel even when they could take split-KV decode
 MIN_CONTEXT = 8192   # kept for API compatibility: the HIP prefill has no context threshold
@@ -55,7 +55,9 @@ def prefill_attention(q, k_cache, v_cache, k_scale_cache, v_scale_cache, out, *,
     domain, softmax_scale multiplies q.k in that domain. With rht_signs the result is rotated back,
     out = (o H D) * rht_out_scale. When the chunk alone cannot fill the GPU, the keys are split over workgroups
     (num_splits, 0 = automatic) and merged; the fp32 partials go to a workspace from torch's caching allocator.
-    max_seqlen_k bounds the automatic split count; without it the block table's capacity stands in (no host sync)."""
+    max_seqlen_k bounds the automatic split count; without it the block table's capacity stands in (no host sync).
+    Head 512, or more than 12 query heads per KV head, runs the split-KV decode kernel over causal query slices of
+    the chunk and merges (the library picks the path)."""
     hs = q.shape[2]
     cache = _hip.paged_cache(k_cache, v_cache, k_scale_cache, v_scale_cache, hs)
     if max_seqlen_k is None:
@@ -80,9 +82,6 @@ def prefill_attention(q, k_cache, v_cache, k_scale_cache, v_scale_cache, out, *,
     args.rht_out_scale = float(rht_out_scale)
     lib = _hip.lib()
     need = lib.qp_prefill_workspace_size(cache, args)
-    if num_splits and num_splits > 1:
-        rows = q.shape[0] * q.shape[1] * num_splits
-        need = rows * hs * 4 + 2 * rows * 4
     ws = torch.empty(need, dtype=torch.uint8, device=q.device) if need > 0 else None
     args.workspace = _hip.ptr(ws)
     args.workspace_bytes = need
