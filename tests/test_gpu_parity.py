@@ -316,7 +316,7 @@ def test_unified_attention_decode_matches_fp64(device, fmt, qlen):
     assert err < 5e-3, err
 
 
-def _host_cache(kc, vc, ks, vs, fmt):
+def _host_cache(kc, vc, ks, vs, fmt, hs=HS):
     """The byte cache behind the views, copied to the host as a numpy (blocks, heads, slots, cell) array."""
     import torch
     st = kc.untyped_storage()
@@ -325,7 +325,7 @@ def _host_cache(kc, vc, ks, vs, fmt):
     base.set_(st, 0, (nbytes,), (1,))
     arr = base.cpu().numpy()
     nb, bs, nkv = kc.shape[0], kc.shape[1], kc.shape[2]
-    cell = O.int4_cell_bytes(HS) if fmt == "int4" else O.k8v4_cell_bytes(HS)
+    cell = O.int4_cell_bytes(hs) if fmt == "int4" else O.k8v4_cell_bytes(hs)
     return arr.reshape(nb, nkv, bs, cell)
 
 
@@ -485,38 +485,40 @@ def test_prefill_span_and_row_loaders_agree(device, monkeypatch):
 
 
 @pytest.mark.parametrize("fmt", ["int4", "int8"])
-def test_unified_attention_prefill_matches_fp64(device, fmt):
-    """tests/test_int4_kv.py:172-191 prefill rows: a 256-token chunk over a 6000-token context through the router."""
+@pytest.mark.parametrize("nq,nkv,hs", [(NQ, NKV, HS), (16, 2, 512)], ids=["head256", "head512"])
+def test_unified_attention_prefill_matches_fp64(device, fmt, nq, nkv, hs):
+    """tests/test_int4_kv.py:172-191 prefill rows: a 256-token chunk over a 6000-token context through the router;
+    head 512 with 16 / 2 heads as tests/test_int4_kv.py:194-210 and tests/test_k8v4_kv.py:208-225."""
     import torch
 
     from vllm_quantpack.attention import int4_kv
     rng = np.random.default_rng(205)
     n, bs, qlen = 6000, 16, 256
     nb = -(-n // bs)
-    kv_np = O.new_cache(nb, NKV, bs, O.int4_cell_bytes(HS) if fmt == "int4" else O.k8v4_cell_bytes(HS))
-    _, (kc, vc, ks, vs) = torch_cache(kv_np, HS, fmt, device)
+    kv_np = O.new_cache(nb, nkv, bs, O.int4_cell_bytes(hs) if fmt == "int4" else O.k8v4_cell_bytes(hs))
+    _, (kc, vc, ks, vs) = torch_cache(kv_np, hs, fmt, device)
     g = torch.Generator(device=device).manual_seed(1)
-    k = torch.randn((n, NKV, HS), generator=g, device=device, dtype=torch.bfloat16)
-    v = torch.randn((n, NKV, HS), generator=g, device=device, dtype=torch.bfloat16)
+    k = torch.randn((n, nkv, hs), generator=g, device=device, dtype=torch.bfloat16)
+    v = torch.randn((n, nkv, hs), generator=g, device=device, dtype=torch.bfloat16)
     int4_kv.reshape_and_cache_int4(k, v, kc, vc, torch.arange(n, device=device), k_scale_cache=ks,
                                    v_scale_cache=vs)
-    q = torch.randn((qlen, NQ, HS), generator=g, device=device, dtype=torch.bfloat16)
+    q = torch.randn((qlen, nq, hs), generator=g, device=device, dtype=torch.bfloat16)
     out = torch.empty_like(q)
-    segm = (torch.empty((32, NQ, 16, HS), dtype=torch.float32, device=device),
-            torch.empty((32, NQ, 16), dtype=torch.float32, device=device),
-            torch.empty((32, NQ, 16), dtype=torch.float32, device=device))
+    segm = (torch.empty((32, nq, 16, hs), dtype=torch.float32, device=device),
+            torch.empty((32, nq, 16), dtype=torch.float32, device=device),
+            torch.empty((32, nq, 16), dtype=torch.float32, device=device))
     int4_kv.unified_attention_int4(
         q, kc, vc, out, cu_seqlens_q=i32([0, qlen], device), max_seqlen_q=qlen, seqused_k=i32([n], device),
-        max_seqlen_k=n, softmax_scale=HS ** -0.5, window_size=(-1, -1),
+        max_seqlen_k=n, softmax_scale=hs ** -0.5, window_size=(-1, -1),
         block_table=torch.arange(nb, dtype=torch.int32, device=device)[None], softcap=0.0, sinks=None,
         alibi_slopes=None, use_alibi_sqrt=False, qq_bias=None, output_scale=None, mm_prefix_range=None,
         k_scale_cache=ks, v_scale_cache=vs, seq_threshold_3D=32, num_par_softmax_segments=16,
         softmax_segm_output=segm[0], softmax_segm_max=segm[1], softmax_segm_expsum=segm[2])
     torch.cuda.synchronize()
     views = O.int4_views if fmt == "int4" else O.k8v4_views
-    K, V = O.dequant_f64(views(_host_cache(kc, vc, ks, vs, fmt), HS), np.arange(nb), n)
+    K, V = O.dequant_f64(views(_host_cache(kc, vc, ks, vs, fmt, hs), hs), np.arange(nb), n)
     qr = O.rht(to_f32(q).astype(np.float64))
-    ref = O.rht(O.attention_f64(qr, K, V, n, HS ** -0.5 / HS), inverse=True) / HS
+    ref = O.rht(O.attention_f64(qr, K, V, n, hs ** -0.5 / hs), inverse=True) / hs
     err = O.relerr(to_f32(out), ref)
     assert err < 5e-3, err
 
