@@ -228,7 +228,10 @@ __device__ __forceinline__ float2 value_floats_paired(uint32_t word, bool ok) {
 // on them is placed by hand (wait_vmcnt before a stage is read, wait_lgkm0 before a stage is refilled).
 __device__ __forceinline__ void dma16(const uint8_t *src, uint8_t *dst) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)dst;
+  // readfirstlane right at the use: the LDS base is uniform, and an SGPR defined here cannot have been spilled to a
+  // VGPR on the way (the "s" operand must be an SGPR)
+  const uint32_t lds =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)dst);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
                : "memory", "m0");
 #endif
@@ -238,7 +241,8 @@ __device__ __forceinline__ void dma16(const uint8_t *src, uint8_t *dst) {
 // streams through the caches instead of displacing what is reused, and measures about 13 % more bandwidth from HBM.
 __device__ __forceinline__ void dma16_stream(const uint8_t *src, uint8_t *dst) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)dst;
+  const uint32_t lds =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)dst);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(lds)
                : "memory", "m0");
 #endif

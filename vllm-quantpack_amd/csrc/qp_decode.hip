@@ -697,24 +697,37 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
   const int seq = d.seq, q0 = d.q0, T = d.T, n = d.n, kstart = d.kstart, kend = d.kend;
   const int col = lane & 15, g = lane >> 4;
 
-  WaveState<HS, KFMT, NCT> st;
-  init_state(st, p, q0, T, n, h, G, col, g);
+  // Chunks are handed out in key order: the first kStages of every wave statically (chunk w + s * WAVES), the rest
+  // from a workgroup counter whenever a stage frees up. Waves whose first copies got out earlier take more of the
+  // segment, so all waves of the workgroup finish together.
+  __shared__ int next_chunk;
+  if (threadIdx.x == 0) next_chunk = kStages * WAVES;
+  __syncthreads();
 
   uint8_t *wl = smem + w * kStages * 2 * Sh::kHalf;
   const int32_t *trow = p.table + (int64_t)seq * p.table_stride;
   const int nchunks = (kend - kstart + kChunk - 1) / kChunk;
-  const int mine = nchunks > w ? (nchunks - w + WAVES - 1) / WAVES : 0;  // chunks of this wave
   const int causal_lim = min(kend, n - T + 1);
   constexpr int kWordK = Sh::kKeyBytes, kWordV = Sh::kCell - 4;
 
-  if (mine > 0) issue_span_dma<Sh>(p, trow, kstart + w * kChunk, kend, h, lane, wl);
-  if (kStages > 1 && mine > 1)
-    issue_span_dma<Sh>(p, trow, kstart + (w + WAVES) * kChunk, kend, h, lane, wl + 2 * Sh::kHalf);
-  for (int i = 0; i < mine; ++i) {
-    const int k0 = kstart + (w + i * WAVES) * kChunk;
-    uint8_t *stage = wl + (i % kStages) * 2 * Sh::kHalf;
-    float4 *fl = kfl[w][i % kStages];
-    if (kStages > 1 && i + 1 < mine) wait_vmcnt<Sh::kDmaPerChunk>();
+  // The query rows load first: their wait is on the vm counter, which would otherwise also wait for the copies.
+  WaveState<HS, KFMT, NCT> st;
+  init_state(st, p, q0, T, n, h, G, col, g);
+  int cid[kStages];  // chunk in each stage (issue order alternates between stages), -1 = empty
+#pragma unroll
+  for (int s0 = 0; s0 < kStages; ++s0) {
+    cid[s0] = w + s0 * WAVES < nchunks ? w + s0 * WAVES : -1;
+    if (cid[s0] >= 0) issue_span_dma<Sh>(p, trow, kstart + cid[s0] * kChunk, kend, h, lane, wl + s0 * 2 * Sh::kHalf);
+  }
+
+  // one chunk through stage si; false when the stage is empty (then so is every later one)
+  auto step = [&](const int si) -> bool {
+    const int c = cid[si];
+    if (c < 0) return false;
+    const int k0 = kstart + c * kChunk;
+    uint8_t *stage = wl + si * 2 * Sh::kHalf;
+    float4 *fl = kfl[w][si];
+    if (kStages > 1 && cid[(si + 1) % kStages] >= 0) wait_vmcnt<Sh::kDmaPerChunk>();  // the other stage is younger
     else wait_vmcnt<0>();
     {  // per-key scalars from the words now in LDS
       const int kk = lane & 31;
@@ -727,13 +740,26 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
     wave_sync();
     ChunkState<HS, NCT> cr;
     chunk_reads<HS, KFMT, NCT, Sh::kCell, Sh::kCell>(st, cr, stage, stage + Sh::kKeyBytes + 4, col, g);
-    if (i + kStages < mine) {
+    int nc = 0;
+    if (lane == 0) nc = atomicAdd(&next_chunk, 1);
+    nc = uniform(nc);
+    if (nc < nchunks) {
       // the stage's K and V codes are in registers now: refill it before the softmax and PV run
       wait_lgkm0();  // every read of this stage has returned before the DMA may overwrite it
       wave_sync();
-      issue_span_dma<Sh>(p, trow, k0 + kStages * WAVES * kChunk, kend, h, lane, stage);
+      issue_span_dma<Sh>(p, trow, kstart + nc * kChunk, kend, h, lane, stage);
+      cid[si] = nc;
+    } else {
+      cid[si] = -1;
     }
     chunk_finish<HS, KFMT, NCT>(st, cr, reinterpret_cast<const uint8_t *>(fl), k0, kend, causal_lim, g);
+    return true;
+  };
+  for (;;) {
+    if (!step(0)) break;
+    if constexpr (kStages > 1) {
+      if (!step(1)) break;
+    }
   }
   if constexpr (kParMerge) finish_workgroup<HS, KFMT, NCT, WAVES>(st, smem, p, w, col, g, q0, T, G, h, seg_idx);
   else finish_workgroup_serial<HS, KFMT, NCT, WAVES>(st, smem, p, w, col, g, q0, T, G, h, seg_idx);
