@@ -805,7 +805,10 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
   const int active = seg > 0 ? min(p.num_segments, (n + seg - 1) / seg) : 0;
   const float *mrow = p.smax + (int64_t)tok * p.sts0 + (int64_t)head * p.sts1;
   const float *lrow = p.ssum + (int64_t)tok * p.sts0 + (int64_t)head * p.sts1;
-  const int quads = p.head_size / 4;
+  // without the rotation the channels split over gridDim.z workgroups (more CUs reading the partials); the rotation
+  // needs the whole row in one workgroup
+  const int width = p.head_size / gridDim.z, c0 = blockIdx.z * width;
+  const int quads = width / 4;
   const int groups = 256 / quads;
   const int cq = t % quads, sg = t / quads;
   float sgn[4];  // rotation signs of the channels this thread writes, requested with the segment loads
@@ -818,18 +821,23 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
   if (sg < groups) {
     // batches of kBatch segments: every load of a batch is issued before any of it is used
     constexpr int kBatch = 16;
-    const float *orow = p.so + (int64_t)tok * p.sos0 + (int64_t)head * p.sos1 + 4 * cq;
-    for (int s0 = sg; s0 < active; s0 += kBatch * groups) {
+    const float *orow = p.so + (int64_t)tok * p.sos0 + (int64_t)head * p.sos1 + c0 + 4 * cq;
+    // rows are requested for every allocated segment (those past `active` are read but ignored), so the loads do not
+    // wait for the context length
+    for (int s0 = sg; s0 < p.num_segments; s0 += kBatch * groups) {
       float4 v[kBatch];
       float ms[kBatch], ls[kBatch];
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) {
         const int s = s0 + k * groups;
-        const bool ok = s < active;
-        v[k] = ok ? *reinterpret_cast<const float4 *>(orow + (int64_t)s * p.sos2) : make_float4(0.f, 0.f, 0.f, 0.f);
-        ms[k] = ok ? mrow[s] : -INFINITY;
-        ls[k] = ok ? lrow[s] : 0.f;
+        const bool in = s < p.num_segments;
+        v[k] = in ? *reinterpret_cast<const float4 *>(orow + (int64_t)s * p.sos2) : make_float4(0.f, 0.f, 0.f, 0.f);
+        ms[k] = in ? mrow[s] : -INFINITY;
+        ls[k] = in ? lrow[s] : 0.f;
       }
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k)
+        if (s0 + k * groups >= active) ms[k] = -INFINITY;
       float bm = mt;
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) bm = fmaxf(bm, ms[k]);
@@ -897,13 +905,13 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int c = t + 256 * k;
-    if (c < p.head_size) {
+    if (c < width) {
       float x = row[cur][c];
       if constexpr (RHT) x *= sgn[k];
-      p.out[(int64_t)tok * p.os0 + (int64_t)head * p.os1 + c] = f32_to_bf16_bits(x);
+      p.out[(int64_t)tok * p.os0 + (int64_t)head * p.os1 + c0 + c] = f32_to_bf16_bits(x);
     }
   }
-  if (p.lse && t == 0) {
+  if (p.lse && t == 0 && blockIdx.z == 0) {
     const float M = stat[0], L = stat[1];
     p.lse[(int64_t)tok * p.ls0 + (int64_t)head * p.ls1] =
         (M == -INFINITY || L <= 0.f) ? -INFINITY : (M + __log2f(L)) * 0.6931471805599453f;
@@ -1106,7 +1114,10 @@ extern "C" int qp_merge_segments(const qp_merge_args *a, qp_stream_t stream) {
   p.ls1 = a->lse_stride[1];
   p.signs = a->rht_signs;
   p.out_scale = a->rht_out_scale;
-  const dim3 grid(a->num_tokens, a->num_q_heads);
+  // a few rows need the channel split to spread the partial reads over more CUs; many rows fill the device alone
+  const int64_t rows = (int64_t)a->num_tokens * a->num_q_heads;
+  const int parts = (a->rht_signs || rows >= 1024 || a->head_size < 64) ? 1 : 4;
+  const dim3 grid(a->num_tokens, a->num_q_heads, parts);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (a->rht_signs) merge_kernel<true><<<grid, 256, 0, s>>>(p);
   else merge_kernel<false><<<grid, 256, 0, s>>>(p);
