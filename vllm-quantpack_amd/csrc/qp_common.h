@@ -48,6 +48,14 @@ __device__ __forceinline__ uint32_t nib_pair(uint32_t x) {
   return (uint32_t)__builtin_amdgcn_bitop3_b32(x, 0x000F000Fu, 0x43004300u, 0xEA);  // (x & m) | c, one v_bitop3
 }
 
+// The same pair with offset 16 instead of 128: bf16(0x4180 | n << 3) = 16 + n, nibble c of each 16-bit half of x.
+// Sums of P (16 + n) minus P (16 + zp) cancel 8x less than with 128 + n, which matters for accumulations over tens of
+// thousands of keys in fp32.
+__device__ __forceinline__ uint32_t nib_pair16(uint32_t x, int c) {
+  const uint32_t y = c == 0 ? x << 3 : x >> (4 * c - 3);
+  return (uint32_t)__builtin_amdgcn_bitop3_b32(y, 0x00780078u, 0x41804180u, 0xEA);
+}
+
 // ---------------------------------------------------------------------------------------------- MFMA
 
 // D(16x16) += A(16x32) B(32x16), bf16 operands, fp32 accumulation. Lane l supplies row l%16 of A and column l%16

@@ -12,9 +12,11 @@
 // w + 8, so each K / V operand read from LDS feeds NT MFMAs and every K/V tile is dequantised once for all G heads.
 // Per 32-key tile, with one barrier:
 //   * the tile's two 16-key page runs come HBM -> LDS (global_load_lds_dwordx4), up to three tiles ahead;
-//   * all threads unpack the next tile to exact bf16 integers: K rows (channel order permuted like the query
-//     operand), V^T rows (keys in MFMA K-slot order) plus a 17th channel tile whose first row holds 128 + zp_v, so
-//     the zero-point sum sum_k P16_k (128 + zp_v,k) comes out of the PV MFMA instead of the VALU;
+//   * all threads unpack the next tile to exact bf16 integers: K rows (128 + n, channel order permuted like the
+//     query operand), V^T rows (16 + n, keys in MFMA K-slot order) plus a 17th channel tile whose first row holds
+//     16 + zp_v, so the zero-point sum sum_k P16_k (16 + zp_v,k) comes out of the PV MFMA instead of the VALU. The
+//     V offset is 16 rather than 128 because acc - sum P16 (offset + zp) cancels: over the tens of thousands of keys
+//     of one split, fp32 rounding of the offset-128 sums alone measured 0.5-0.9 % of the output;
 //   * each wave runs S^T = K Q^T (v_mfma_f32_16x16x32_bf16, K as the A operand), the softmax in registers and
 //     O^T += V^T P^T with P^T straight from the S^T registers.
 // The unpack of tile i + 1 sits in the same basic blocks as the MFMAs of tile i, so the scheduler interleaves them
@@ -203,8 +205,7 @@ __device__ __forceinline__ void pf_unpack_v(const uint8_t *pk, uint8_t *vt, int 
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       *reinterpret_cast<u32x4_t *>(vt + (4 * q4 + c) * Sh::kVtRow + 16 * ko) =
-          u32x4_t{nib_pair(pr[0] >> (4 * c)), nib_pair(pr[1] >> (4 * c)), nib_pair(pr[2] >> (4 * c)),
-                  nib_pair(pr[3] >> (4 * c))};
+          u32x4_t{nib_pair16(pr[0], c), nib_pair16(pr[1], c), nib_pair16(pr[2], c), nib_pair16(pr[3], c)};
   }
   if (tid < kPfKeys) {
     const int kk = tid;
@@ -223,7 +224,7 @@ __device__ __forceinline__ void pf_unpack_v(const uint8_t *pk, uint8_t *vt, int 
     kf[kPfKeys + kk] = ok ? e : 0.f;
     kf[2 * kPfKeys + kk] = ok ? __uint_as_float(vw & 0xFFFFFFF0u) : 0.f;
     const int slot_off = 16 * ((kk & 15) >> 2) + 2 * ((kk & 3) + 4 * (kk >> 4));
-    *reinterpret_cast<uint16_t *>(vt + HS * Sh::kVtRow + slot_off) = ok ? (uint16_t)(0x4300u | (vw & 0xFu)) : 0;
+    *reinterpret_cast<uint16_t *>(vt + HS * Sh::kVtRow + slot_off) = ok ? (uint16_t)(0x4180u | ((vw & 0xFu) << 3)) : 0;
   }
 }
 
@@ -284,8 +285,7 @@ struct PfStager {
   __device__ __forceinline__ void v_store(int c) {
     const int u = vunit(), ko = u & 3, q4 = u >> 2;
     *reinterpret_cast<u32x4_t *>(vt + (4 * q4 + c) * Sh::kVtRow + 16 * ko) =
-        u32x4_t{nib_pair(pr[0] >> (4 * c)), nib_pair(pr[1] >> (4 * c)), nib_pair(pr[2] >> (4 * c)),
-                nib_pair(pr[3] >> (4 * c))};
+        u32x4_t{nib_pair16(pr[0], c), nib_pair16(pr[1], c), nib_pair16(pr[2], c), nib_pair16(pr[3], c)};
   }
   // per-key scalars: thread kk < 32 owns key kk; the others write the same values to a dummy slot
   __device__ __forceinline__ void s_load() {
@@ -311,7 +311,7 @@ struct PfStager {
     *(own ? kf + 2 * kPfKeys + kk : dummy + 2) = ok ? __uint_as_float(vw & 0xFFFFFFF0u) : 0.f;
     const int slot_off = 16 * ((kk & 15) >> 2) + 2 * ((kk & 3) + 4 * (kk >> 4));
     *reinterpret_cast<uint16_t *>(own ? vt + HS * Sh::kVtRow + slot_off : reinterpret_cast<uint8_t *>(dummy + 3)) =
-        ok ? (uint16_t)(0x4300u | (vw & 0xFu)) : 0;
+        ok ? (uint16_t)(0x4180u | ((vw & 0xFu) << 3)) : 0;
   }
 };
 
