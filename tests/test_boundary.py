@@ -153,6 +153,15 @@ def test_segments_follow_cu_count(monkeypatch, sms, segments):
     assert int4_kv.decode_tiles(sms) == (64, 4, segments)
 
 
+@pytest.mark.parametrize("requested,seqs,heads,sms,want", [(64, 1, 4, 256, 64), (64, 32, 4, 256, 16),
+                                                         (64, 256, 8, 256, 1), (16, 1, 4, 256, 16), (64, 12, 4, 256, 43)])
+def test_decode_segments_follow_the_batch(requested, seqs, heads, sms, want):
+    """The router keeps the caller's segment count for one sequence and lowers it for batches (about 8 workgroups
+    per CU), never above the caller's count (the capacity of its segment buffers)."""
+    from vllm_quantpack.attention import int4_kv
+    assert int4_kv.decode_segments(requested, seqs, heads, sms) == want
+
+
 def test_cell_is_key_bytes_plus_packed_value_plus_two_scales():
     from vllm_quantpack.attention import k8v4_kv
     assert k8v4_kv.cell_bytes(256, 256) == 392

@@ -316,6 +316,59 @@ def test_unified_attention_decode_matches_fp64(device, fmt, qlen):
     assert err < 5e-3, err
 
 
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+def test_unified_attention_decode_batch_matches_fp64(device, fmt):
+    """The router on a ragged batch of 12 sequences (1 or 2 query tokens, 300 to 3000 cached tokens): it lowers the
+    caller's 64 segments to 43 for the batch; every sequence within 0.5 % of fp64."""
+    import torch
+
+    from vllm_quantpack.attention import int4_kv
+    rng = np.random.default_rng(91)
+    seqs, bs = 12, 16
+    T = rng.integers(1, 3, size=seqs)
+    n = rng.integers(300, 3001, size=seqs)
+    nb = -(-n // bs)
+    total = int(nb.sum())
+    kv_np = O.new_cache(total, NKV, bs, O.int4_cell_bytes(HS) if fmt == "int4" else O.k8v4_cell_bytes(HS))
+    _, (kc, vc, ks, vs) = torch_cache(kv_np, HS, fmt, device)
+    pool = rng.permutation(total).astype(np.int32)
+    table = np.zeros((seqs, int(nb.max())), np.int32)
+    at = 0
+    g = torch.Generator(device=device).manual_seed(1)
+    for i in range(seqs):
+        table[i, :nb[i]] = pool[at:at + nb[i]]
+        at += nb[i]
+        slots = torch.as_tensor(table[i, :nb[i]].astype(np.int64), device=device)[:, None] * bs + torch.arange(
+            bs, device=device)
+        slots = slots.flatten()[:n[i]]
+        k = torch.randn((int(n[i]), NKV, HS), generator=g, device=device, dtype=torch.bfloat16)
+        v = torch.randn((int(n[i]), NKV, HS), generator=g, device=device, dtype=torch.bfloat16)
+        int4_kv.reshape_and_cache_int4(k, v, kc, vc, slots, k_scale_cache=ks, v_scale_cache=vs)
+    q = torch.randn((int(T.sum()), NQ, HS), generator=g, device=device, dtype=torch.bfloat16)
+    cu = np.concatenate(([0], np.cumsum(T))).astype(np.int32)
+    S, rows = 64, int(T.sum())
+    segm = (torch.empty((rows, NQ, S, HS), dtype=torch.float32, device=device),
+            torch.empty((rows, NQ, S), dtype=torch.float32, device=device),
+            torch.empty((rows, NQ, S), dtype=torch.float32, device=device))
+    out = torch.empty_like(q)
+    assert int4_kv.decode_segments(S, seqs, NKV, torch.cuda.get_device_properties(device).multi_processor_count) < S
+    int4_kv.unified_attention_int4(
+        q, kc, vc, out, cu_seqlens_q=i32(cu, device), max_seqlen_q=int(T.max()), seqused_k=i32(n, device),
+        max_seqlen_k=int(n.max()), softmax_scale=HS ** -0.5, window_size=(-1, -1), block_table=i32(table, device),
+        softcap=0.0, sinks=None, alibi_slopes=None, use_alibi_sqrt=False, qq_bias=None, output_scale=None,
+        mm_prefix_range=None, k_scale_cache=ks, v_scale_cache=vs, seq_threshold_3D=rows, num_par_softmax_segments=S,
+        softmax_segm_output=segm[0], softmax_segm_max=segm[1], softmax_segm_expsum=segm[2])
+    torch.cuda.synchronize()
+    views = O.int4_views if fmt == "int4" else O.k8v4_views
+    root = _host_cache(kc, vc, ks, vs, fmt)
+    got = to_f32(out)
+    qr = O.rht(to_f32(q).astype(np.float64))
+    for i in range(seqs):
+        K, V = O.dequant_f64(views(root, HS), table[i], int(n[i]))
+        ref = O.rht(O.attention_f64(qr[cu[i]:cu[i + 1]], K, V, int(n[i]), HS ** -0.5 / HS), inverse=True) / HS
+        assert O.relerr(got[cu[i]:cu[i + 1]], ref) < 5e-3, i
+
+
 def _host_cache(kc, vc, ks, vs, fmt, hs=HS):
     """The byte cache behind the views, copied to the host as a numpy (blocks, heads, slots, cell) array."""
     import torch
