@@ -111,7 +111,7 @@ def mfma_hazards(asm):
 
 def _check_inline_mfma(src, verbose):
     text = open(src).read()
-    if 'asm volatile("v_mfma' not in text:
+    if not re.search(r'asm\s+volatile\s*\(\s*"[^;]*?v_mfma', text):
         return
     out = os.path.join(OBJ, os.path.basename(src).replace(".hip", ".gfx.s"))
     cmd = [hipcc(), *_flags(src), "--cuda-device-only", "-S", src, "-o", out]

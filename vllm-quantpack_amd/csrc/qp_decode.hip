@@ -165,10 +165,12 @@ struct ChunkState {
   uint32_t vx[HS / 64][4];  // V codes: [channel block b][key pair d], two keys x four channels (nibbles) each
 };
 
-// kb/vb: LDS rows of the chunk's 32 keys (key kk at kb + kk * KSTR, vb + kk * VSTR).
-template <int HS, int KFMT, int NCT, int KSTR, int VSTR>
+// kb/vb: LDS rows of the chunk's 32 keys (key kk at kb + kk * KSTR, vb + kk * VSTR). With QL the query operands
+// are read from LDS (ql: the lane's operand (ct, mi) at ql[(ct * HS / 32 + mi) * 64]) instead of st.qop.
+template <int HS, int KFMT, int NCT, int KSTR, int VSTR, bool QL = false>
 __device__ __forceinline__ void chunk_reads(const WaveState<HS, KFMT, NCT> &st, ChunkState<HS, NCT> &cr,
-                                            const uint8_t *kb, const uint8_t *vb, int col, int g) {
+                                            const uint8_t *kb, const uint8_t *vb, int col, int g,
+                                            const bf16x8_t *ql = nullptr) {
   constexpr int kKeyBytes = KFMT == QP_CODES_INT4 ? HS / 2 : HS;
   constexpr int kNmi = HS / 32, kNb = HS / 64;
   f32x4_t (&sacc)[NCT][2] = cr.sacc;
@@ -191,7 +193,8 @@ __device__ __forceinline__ void chunk_reads(const WaveState<HS, KFMT, NCT> &st, 
         const bf16x8_t kop = as_bf16x8(u32x4_t{nib_pair(x), nib_pair(y), nib_pair(x >> 8), nib_pair(y >> 8)});
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct)
-          sacc[ct][sub] = mfma16x16x32(kop, st.qop[ct][mi], mi == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sacc[ct][sub]);
+          sacc[ct][sub] = mfma16x16x32(kop, QL ? ql[(ct * kNmi + mi) * 64] : st.qop[ct][mi],
+                                       mi == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sacc[ct][sub]);
       }
     } else {
 #pragma unroll
@@ -206,7 +209,8 @@ __device__ __forceinline__ void chunk_reads(const WaveState<HS, KFMT, NCT> &st, 
         const bf16x8_t kop = as_bf16x8(y);
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct)
-          sacc[ct][sub] = mfma16x16x32(kop, st.qop[ct][mi], mi == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sacc[ct][sub]);
+          sacc[ct][sub] = mfma16x16x32(kop, QL ? ql[(ct * kNmi + mi) * 64] : st.qop[ct][mi],
+                                       mi == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sacc[ct][sub]);
       }
     }
   }
@@ -225,10 +229,70 @@ __device__ __forceinline__ void chunk_reads(const WaveState<HS, KFMT, NCT> &st, 
     }
 }
 
+// Two row tiles up to head 256 exceed the 256 architectural VGPRs and run one wave per SIMD. Left to the compiler,
+// their O^T accumulators live in AGPRs between chunks but are copied to VGPRs for every accumulation (about 170
+// extra VALU instructions per chunk). These shapes therefore accumulate through inline-assembly MFMAs whose C and D
+// operands are AGPRs, so the tiles never leave that file except for a rescale of the running maximum and the final
+// merge (4 % faster on 262144 keys with 4 query tokens). The other shapes measured faster with the compiler's MFMAs
+// (one row tile at head 512, int8 keys at head 256), and two row tiles at head 512 must stay with the compiler:
+// their 256 accumulator registers fill the AGPR file, the register allocator then moves tiles out between the
+// accumulations, and only compiler-visible MFMAs keep those moves behind the required wait states.
+template <int HS, int KFMT, int NCT>
+constexpr bool acc_in_agprs() {
+  return NCT == 2 && HS <= 256;
+}
+
+// One channel tile of O^T += V^T P^T for every row tile, on AGPR accumulators. The compiler does not see these as
+// MFMAs, so the wait states are explicit: 2 before them (vop was just written by the VALU; an AGPR written by a
+// rescale is read as C), and, after the chunk's last tile, 18 (an 8-pass XDL result) before anything else may touch
+// the accumulators. Successive tiles of one chunk use disjoint accumulators.
+template <int NCT, int N>
+__device__ __forceinline__ void pv_tile_agpr(f32x4_t (&acc)[NCT][N], int i, bf16x8_t vop, const u32x4_t (&pop)[NCT],
+                                             bool last) {
+  static_assert(NCT == 1 || NCT == 2, "row tiles");
+  if constexpr (NCT == 1) {
+    if (last)
+      asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 1"
+                   : "+a"(acc[0][i]) : "v"(vop), "v"(pop[0]));
+    else
+      asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc[0][i]) : "v"(vop), "v"(pop[0]));
+  } else {
+    if (last)
+      asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %2, %3, %0\n\tv_mfma_f32_16x16x32_bf16 %1, %2, %4, %1\n\t"
+                   "s_nop 7\n\ts_nop 7\n\ts_nop 1"
+                   : "+a"(acc[0][i]), "+a"(acc[1][i]) : "v"(vop), "v"(pop[0]), "v"(pop[1]));
+    else
+      asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %2, %3, %0\n\tv_mfma_f32_16x16x32_bf16 %1, %2, %4, %1"
+                   : "+a"(acc[0][i]), "+a"(acc[1][i]) : "v"(vop), "v"(pop[0]), "v"(pop[1]));
+  }
+}
+
+// acc *= alpha on AGPR tiles, one tile at a time through the lane's 16 bytes of LDS at rs. Tiles move between the
+// AGPRs and LDS only inside assembly blocks (LDS loads and stores take AGPR data): any C++ access to an element makes
+// the register allocator keep a VGPR copy of every tile and refresh it at each chunk, although the rescale runs only a
+// few times per segment. The last accumulation reached this block at least 18 wait states earlier (the chunk's last
+// PV tile ends with them); the next one waits 2 after the reload (pv_tile_agpr), which the lgkm wait has completed.
+template <int N>
+__device__ __forceinline__ void scale_agpr(f32x4_t (&acc)[N], float alpha, f32x4_t *rs) {
+  const uint32_t at = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) f32x4_t *)rs;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    asm volatile("ds_write_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" ::"v"(at), "a"(acc[i]) : "memory");
+    f32x4_t t = *reinterpret_cast<volatile f32x4_t *>(rs);
+    t[0] *= alpha;
+    t[1] *= alpha;
+    t[2] *= alpha;
+    t[3] *= alpha;
+    *reinterpret_cast<volatile f32x4_t *>(rs) = t;
+    asm volatile("s_waitcnt lgkmcnt(0)\n\tds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=a"(acc[i]) : "v"(at) : "memory");
+  }
+}
+
 // Softmax of the chunk and O^T += V^T P^T; fb: float4 of per-key scalars per key.
 template <int HS, int KFMT, int NCT>
 __device__ __forceinline__ void chunk_finish(WaveState<HS, KFMT, NCT> &st, const ChunkState<HS, NCT> &cr,
-                                             const uint8_t *fb, int k0, int kend, int causal_lim, int g) {
+                                             const uint8_t *fb, int k0, int kend, int causal_lim, int g,
+                                             f32x4_t *rs) {
   constexpr int kNb = HS / 64;
   const f32x4_t (&sacc)[NCT][2] = cr.sacc;
 
@@ -270,8 +334,12 @@ __device__ __forceinline__ void chunk_finish(WaveState<HS, KFMT, NCT> &st, const
       const float alpha = st.m[ct] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m[ct] - m_new);
       st.l[ct] *= alpha;
       st.c[ct] *= alpha;
+      if constexpr (acc_in_agprs<HS, KFMT, NCT>()) {
+        scale_agpr(st.acc[ct], alpha, rs);
+      } else {
 #pragma unroll
-      for (int i = 0; i < kNb * 4; ++i) st.acc[ct][i] *= alpha;
+        for (int i = 0; i < kNb * 4; ++i) st.acc[ct][i] *= alpha;
+      }
       st.m[ct] = m_new;
     }
     const float mu = st.m[ct] == -INFINITY ? 0.f : st.m[ct];
@@ -302,9 +370,13 @@ __device__ __forceinline__ void chunk_finish(WaveState<HS, KFMT, NCT> &st, const
 #pragma unroll
       for (int d = 0; d < 4; ++d) vv[d] = nib_pair(cr.vx[b][d] >> (4 * c));
       const bf16x8_t vop = as_bf16x8(vv);
+      if constexpr (acc_in_agprs<HS, KFMT, NCT>()) {
+        pv_tile_agpr<NCT>(st.acc, b * 4 + c, vop, pop, b == kNb - 1 && c == 3);
+      } else {
 #pragma unroll
-      for (int ct = 0; ct < NCT; ++ct)
-        st.acc[ct][b * 4 + c] = mfma16x16x32(vop, as_bf16x8(pop[ct]), st.acc[ct][b * 4 + c]);
+        for (int ct = 0; ct < NCT; ++ct)
+          st.acc[ct][b * 4 + c] = mfma16x16x32(vop, as_bf16x8(pop[ct]), st.acc[ct][b * 4 + c]);
+      }
     }
   }
 }
@@ -312,10 +384,11 @@ __device__ __forceinline__ void chunk_finish(WaveState<HS, KFMT, NCT> &st, const
 // Both parts back to back, for loaders whose LDS rows are not refilled during the chunk.
 template <int HS, int KFMT, int NCT, int KSTR, int VSTR>
 __device__ __forceinline__ void compute_chunk(WaveState<HS, KFMT, NCT> &st, const uint8_t *kb, const uint8_t *vb,
-                                              const uint8_t *fb, int k0, int kend, int causal_lim, int col, int g) {
+                                              const uint8_t *fb, int k0, int kend, int causal_lim, int col, int g,
+                                              f32x4_t *rs) {
   ChunkState<HS, NCT> cr;
   chunk_reads<HS, KFMT, NCT, KSTR, VSTR>(st, cr, kb, vb, col, g);
-  chunk_finish<HS, KFMT, NCT>(st, cr, fb, k0, kend, causal_lim, g);
+  chunk_finish<HS, KFMT, NCT>(st, cr, fb, k0, kend, causal_lim, g, rs);
 }
 
 // ------------------------------------------------------------------------ merge of the waves, partial out
@@ -582,6 +655,7 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(const DecodeParams p) 
   constexpr int kLds = kWaves * Sh::kStage > merge_serial_lds_bytes<HS, NCT>() ? kWaves * Sh::kStage
                                                                                 : merge_serial_lds_bytes<HS, NCT>();
   __shared__ __attribute__((aligned(16))) uint8_t smem[kLds];
+  __shared__ f32x4_t rsc[kWaves][acc_in_agprs<HS, KFMT, NCT>() ? 64 : 1];  // rescale of AGPR accumulators
 
   const int lane = threadIdx.x & 63;
   const int w = uniform(threadIdx.x >> 6);
@@ -626,7 +700,7 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(const DecodeParams p) 
     if (ci + kWaves < nchunks)
       load_rows<Sh>(regs, p, trow, k0 + kWaves * kChunk, kend, h, lane, koff_lane, voff_lane);
     compute_chunk<HS, KFMT, NCT, Sh::kKRow, Sh::kVRow>(st, wl, wl + Sh::kVOff, wl + Sh::kFOff, k0, kend, causal_lim,
-                                                       col, g);
+                                                       col, g, &rsc[w][lane]);
   }
   finish_workgroup_serial<HS, KFMT, NCT, kWaves>(st, smem, p, w, col, g, q0, T, G, h, seg_idx);
 }
@@ -687,6 +761,11 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
   // scalar stores from the in-flight copies and does not wait for the copies before them
   __shared__ __attribute__((aligned(16))) uint8_t smem[kLds];
   __shared__ __attribute__((aligned(16))) float4 kfl[WAVES][kStages][kChunk];
+  __shared__ f32x4_t rsc[WAVES][acc_in_agprs<HS, KFMT, NCT>() ? 64 : 1];  // rescale of AGPR accumulators
+  // Two row tiles of query operands (64 registers at head 256) are read from LDS instead of being held: the wave
+  // state then fits the VGPRs without spills. Every wave of the workgroup attends the same rows.
+  constexpr bool kQL = NCT == 2 && HS <= 256;
+  __shared__ bf16x8_t qsh[kQL ? NCT * (HS / 32) * 64 : 1];
 
   const int lane = threadIdx.x & 63;
   const int w = uniform(threadIdx.x >> 6);
@@ -713,6 +792,13 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
   // The query rows load first: their wait is on the vm counter, which would otherwise also wait for the copies.
   WaveState<HS, KFMT, NCT> st;
   init_state(st, p, q0, T, n, h, G, col, g);
+  if constexpr (kQL) {
+    // every wave stores the same operands, and reads back only what its own lanes stored
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+      for (int mi = 0; mi < HS / 32; ++mi) qsh[(ct * (HS / 32) + mi) * 64 + lane] = st.qop[ct][mi];
+  }
   int cid[kStages];  // chunk in each stage (issue order alternates between stages), -1 = empty
 #pragma unroll
   for (int s0 = 0; s0 < kStages; ++s0) {
@@ -739,7 +825,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
     }
     wave_sync();
     ChunkState<HS, NCT> cr;
-    chunk_reads<HS, KFMT, NCT, Sh::kCell, Sh::kCell>(st, cr, stage, stage + Sh::kKeyBytes + 4, col, g);
+    chunk_reads<HS, KFMT, NCT, Sh::kCell, Sh::kCell, kQL>(st, cr, stage, stage + Sh::kKeyBytes + 4, col, g,
+                                                          qsh + lane);
     int nc = 0;
     if (lane == 0) nc = atomicAdd(&next_chunk, 1);
     nc = uniform(nc);
@@ -752,7 +839,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
     } else {
       cid[si] = -1;
     }
-    chunk_finish<HS, KFMT, NCT>(st, cr, reinterpret_cast<const uint8_t *>(fl), k0, kend, causal_lim, g);
+    chunk_finish<HS, KFMT, NCT>(st, cr, reinterpret_cast<const uint8_t *>(fl), k0, kend, causal_lim, g,
+                                &rsc[w][lane]);
     return true;
   };
   for (;;) {
