@@ -191,10 +191,11 @@ def test_decode_plan_graph_replays(device):
 
 
 @pytest.mark.parametrize("fmt", ["int4", "int8"])
-@pytest.mark.parametrize("T", [1, 2, 4])
+@pytest.mark.parametrize("T", [1, 2, 3, 4])
 def test_decode_head_512(device, fmt, T):
     """Head 512 with 8 query heads per KV head (Gemma 4 global layers: tests/test_int4_kv.py:194-210,
-    tests/test_k8v4_kv.py:208-225); 4 tokens make 32 query rows, two row tiles."""
+    tests/test_k8v4_kv.py:208-225). 3 and 4 tokens make 24 / 32 query rows: they run as workgroups of two tokens
+    (one row tile each), the last group of 3 tokens holding a single token."""
     rng = np.random.default_rng(300 + T + (10 if fmt == "int8" else 0))
     out, emu, ref, _ = _decode_case(device, rng, fmt, [(T, 3000), (1, 900)], nq=16, nkv=2, hs=512, segments=6)
     assert O.relerr(out, emu) < 1e-2

@@ -54,6 +54,9 @@ struct DecodeParams {
   // Query slices (prefill through the split-KV kernel): when set, workgroup z takes slice z = (sequence, first token
   // index, token count, context of its last token) instead of sequence z; count 0 = nothing to do.
   const int4 *slices;
+  // Token groups (no slices): when tok_group > 0, workgroup z takes tokens [g * tok_group, (g + 1) * tok_group) of
+  // sequence z / tok_groups, g = z % tok_groups, so that the query rows of a workgroup fit fewer row tiles.
+  int32_t tok_group, tok_groups;
 };
 
 // The work of one workgroup: query tokens [q0, q0 + T) of sequence seq, context n for its last token, keys
@@ -74,6 +77,14 @@ __device__ __forceinline__ bool decode_work(const DecodeParams &p, int G, int h,
     d.n = sl.w;
     if (d.T <= 0) return false;
     nfull = p.used_k[d.seq];
+  } else if (p.tok_group > 0) {
+    d.seq = blockIdx.z / p.tok_groups;
+    const int t0 = (blockIdx.z - d.seq * p.tok_groups) * p.tok_group;
+    const int qa = p.cu_q[d.seq], tf = p.cu_q[d.seq + 1] - qa;
+    d.q0 = qa + t0;
+    d.T = min(p.tok_group, tf - t0);
+    nfull = p.used_k[d.seq];
+    d.n = nfull - tf + t0 + d.T;  // context of the group's last token
   } else {
     d.seq = blockIdx.z;
     d.q0 = p.cu_q[d.seq];
@@ -86,7 +97,7 @@ __device__ __forceinline__ bool decode_work(const DecodeParams &p, int G, int h,
   d.kstart = seg_idx * seg;
   d.kend = min(d.n, d.kstart + seg);
   if (d.kstart < d.kend) return true;
-  if (p.slices && d.kstart < nfull) {
+  if ((p.slices || p.tok_group > 0) && d.kstart < nfull) {
     for (int r = threadIdx.x; r < d.T * G; r += blockDim.x) {
       const int64_t o = (int64_t)(d.q0 + r / G) * p.sts0 + (int64_t)(h * G + r % G) * p.sts1 + seg_idx;
       p.smax[o] = -INFINITY;
@@ -1162,8 +1173,17 @@ extern "C" int qp_decode_splitkv(const qp_paged_cache *cache, const qp_decode_ar
   p.num_segments = a->num_segments;
   p.scale_log2 = a->softmax_scale * kLog2e;
   p.slices = nullptr;
-  const int nct = rows > 16 ? 2 : 1;
-  const dim3 grid(a->num_segments, cache->num_kv_heads, a->num_seqs);
+  p.tok_group = 0;
+  p.tok_groups = 1;
+  int nct = rows > 16 ? 2 : 1;
+  if (nct == 2 && cache->head_size == 512 && G <= 16) {
+    // Two row tiles at head 512 do not fit the registers (the accumulators alone fill the AGPRs); workgroups of
+    // whole tokens with at most 16 rows read the segment once per group instead, which costs far less.
+    p.tok_group = 16 / G;
+    p.tok_groups = (a->max_query_len + p.tok_group - 1) / p.tok_group;
+    nct = 1;
+  }
+  const dim3 grid(a->num_segments, cache->num_kv_heads, a->num_seqs * p.tok_groups);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   return dispatch_hs(cache, p, nct, grid, s);
 }
@@ -1297,6 +1317,8 @@ int slice_prefill(const qp_paged_cache *cache, const qp_prefill_args *a, hipStre
   p.num_segments = L.segments;
   p.scale_log2 = a->softmax_scale * kLog2e;
   p.slices = slices;
+  p.tok_group = 0;
+  p.tok_groups = 1;
   const int nct = L.ts * G > 16 ? 2 : 1;
   st = dispatch_hs(cache, p, nct, dim3(L.segments, cache->num_kv_heads, L.max_slices), s);
   if (st != QP_OK) return st;
