@@ -1063,8 +1063,10 @@ namespace {
 template <int HS, int KFMT, int NCT>
 void launch_decode(const DecodeParams &p, dim3 grid, bool span, hipStream_t s) {
   if (span) {
-    // 8 waves (2 per SIMD) fit the registers of one row tile with int4 keys up to head 256; the others run 4.
-    constexpr int kWaves = (KFMT == QP_CODES_INT4 && NCT == 1 && HS <= 256) ? 8 : 4;
+    // 8 waves (2 per SIMD) fit the registers of one row tile up to head 256; the others run 4. With int8 keys the 8
+    // waves have one stage each (the LDS holds 8 x 12.5 KB chunks either way): 20 % faster than 4 waves of two stages
+    // on a ragged batch of 32 sequences, as the second wave per SIMD hides the first one's dependency chain.
+    constexpr int kWaves = (NCT == 1 && HS <= 256) ? 8 : 4;
     decode_span_kernel<HS, KFMT, NCT, kWaves><<<grid, kWaves * 64, 0, s>>>(p);
   } else if constexpr (HS == 512 && KFMT == QP_CODES_INT8) {
     set_error("qp_decode_splitkv: head 512 with int8 keys needs the standard cell layout");
