@@ -42,12 +42,13 @@ def test_unpack_segment_bit_exact(device, fmt, which, layout, bs):
 
 # ---------------------------------------------------------------------------------------------------- decode
 
-def _decode_case(device, rng, fmt, lens, layout="hnd", bs=16, segments=8, nq=NQ, nkv=NKV, hs=HS, scale=None):
-    """lens = [(T_i, n_i)]: one call over the batch; returns (gpu out, oracle emulation, fp64 refs)."""
+def _decode_case(device, rng, fmt, lens, layout="hnd", bs=16, segments=8, nq=NQ, nkv=NKV, hs=HS, scale=None,
+                 big_keys=()):
+    """lens = [(T_i, n_i)]: one call over the batch; returns (gpu out, oracle emulation, fp64 refs). big_keys =
+    [(first position, count, factor)] multiplies the key scales of those positions of every sequence by factor."""
     nbs = [-(-n // bs) for _, n in lens]
     total = sum(nbs) + 3
     kv, v = random_cache(rng, total, nkv, bs, hs, fmt, layout)
-    _, views = torch_cache(kv, hs, fmt, device)
     pool = rng.permutation(total).astype(np.int32)
     width = max(nbs)
     table = np.zeros((len(lens), width), np.int32)
@@ -55,6 +56,17 @@ def _decode_case(device, rng, fmt, lens, layout="hnd", bs=16, segments=8, nq=NQ,
     for i, nb in enumerate(nbs):
         table[i, :nb] = pool[at:at + nb]
         at += nb
+    for first, count, factor in big_keys:
+        for i in range(len(lens)):
+            for pos in range(first, first + count):
+                blk, slot = table[i, pos // bs], pos % bs
+                words = v.key_word[blk, slot]
+                if fmt == "int4":
+                    big = (words & np.uint32(0xFFFFFFF0)).view(np.float32) * np.float32(factor)
+                    words[:] = (big.view(np.uint32) & np.uint32(0xFFFFFFF0)) | (words & np.uint32(0xF))
+                else:
+                    words[:] = (words.view(np.float32) * np.float32(factor)).view(np.uint32)
+    _, views = torch_cache(kv, hs, fmt, device)
     Ts = [t for t, _ in lens]
     q = O.f32_to_bf16_bits(rng.standard_normal((sum(Ts), nq, hs)).astype(np.float32))
     cu = np.concatenate(([0], np.cumsum(Ts))).astype(np.int32)
@@ -79,6 +91,22 @@ def test_decode_matches_oracle(device, fmt, T):
     out, emu, ref, _ = _decode_case(device, rng, fmt, [(T, 5003)], segments=7)
     assert O.relerr(out, emu) < 1e-2
     assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+@pytest.mark.parametrize("T", [1, 4])
+def test_decode_scores_far_above_the_running_maximum(device, fmt, T):
+    """Two key blocks with larger key scales (int4 8x and 20x, int8 2.5x and 5x) give scores 10-60 (log2 units)
+    above the maximum the waves hold when they reach them, so the accumulators are rescaled mid-segment (by assembly
+    on AGPR tiles for the two row tiles of T = 4: 4 tokens x 6 query heads per KV head). The keys before them keep a share of the probability mass (median
+    1-12 %, up to 38 % and more per row), so a rescale that drops or mis-scales them shows against fp64."""
+    rng = np.random.default_rng(400 + T + (10 if fmt == "int8" else 0))
+    f1, f2 = (8.0, 20.0) if fmt == "int4" else (2.5, 5.0)
+    out, emu, ref, _ = _decode_case(device, rng, fmt, [(T, 4000)], segments=7, nq=12, nkv=2,
+                                    big_keys=[(1504, 16, f1), (2900, 8, f2)])
+    assert np.isfinite(out).all()
+    assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
+    assert O.relerr(out, emu) < 1e-2
 
 
 @pytest.mark.parametrize("layout,bs", [("nhd", 16), ("hnd", 32), ("hnd", 3072), ("nhd", 48)])
