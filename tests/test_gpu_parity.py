@@ -230,9 +230,12 @@ def test_decode_head_512(device, fmt, T):
     assert O.relerr(out, ref) < 5e-3
 
 
-def test_decode_gqa_8_and_head_128(device):
-    rng = np.random.default_rng(51)
-    out, emu, ref, _ = _decode_case(device, rng, "int4", [(4, 2500), (1, 700)], nq=16, nkv=2, hs=128, segments=9)
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+def test_decode_gqa_8_and_head_128(device, fmt):
+    """Head 128, 8 query heads per KV head: 4 tokens are two row tiles (AGPR accumulators), 1 token one row tile
+    (8 waves; one stage each with int8 keys)."""
+    rng = np.random.default_rng(51 + (10 if fmt == "int8" else 0))
+    out, emu, ref, _ = _decode_case(device, rng, fmt, [(4, 2500), (1, 700)], nq=16, nkv=2, hs=128, segments=9)
     assert O.relerr(out, emu) < 1e-2
     assert O.relerr(out, ref) < 5e-3
 
