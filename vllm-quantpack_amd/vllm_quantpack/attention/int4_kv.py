@@ -53,7 +53,7 @@ def segments_for(sms):
 def decode_segments(requested, num_seqs, num_kv_heads, sms):
     """Segments per (sequence, KV head) the split-KV decode actually uses: the caller's count (the capacity of its
     segment buffers), lowered for batches so that one launch holds about 8 workgroups per CU. Longer segments stream
-    more keys per workgroup: the 32-request ragged k8v4 batch runs 289 us at 16 segments against 375 us at 64, while a
+    more keys per workgroup: the 32-request ragged k8v4 batch runs 232 us at 16 segments against 331 us at 64, while a
     single sequence keeps all 64 (4 KV heads x 64 = one workgroup per CU). Any count gives the same result up to fp32
     rounding (the merge takes the same count)."""
     want = -(-8 * max(1, sms) // max(1, num_seqs * num_kv_heads))
