@@ -960,24 +960,44 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
       }
     }
   }
+  // The states of one channel quad (threads cq + quads * k) combine across the wave by lane exchanges first (every
+  // lane ends with its quad's wave state), then across the 4 waves through LDS: at most 4 serial steps, whatever the
+  // number of groups.
+  for (int off = quads; off < 64; off <<= 1) {
+    const float mo = shfl_xor_f(mt, off), lo = shfl_xor_f(lt, off);
+    const float4 ao = make_float4(shfl_xor_f(a.x, off), shfl_xor_f(a.y, off), shfl_xor_f(a.z, off),
+                                  shfl_xor_f(a.w, off));
+    const float M = fmaxf(mt, mo);
+    const float f0 = mt == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mt - M);
+    const float f1 = mo == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mo - M);
+    a = make_float4(fmaf(a.x, f0, ao.x * f1), fmaf(a.y, f0, ao.y * f1), fmaf(a.z, f0, ao.z * f1),
+                    fmaf(a.w, f0, ao.w * f1));
+    lt = fmaf(lt, f0, lo * f1);
+    mt = M;
+  }
   part[t] = a;
   pm[t] = mt;
   pl[t] = lt;
   __syncthreads();
   if (t < quads) {
+    const int stride = quads > 64 ? quads : 64, count = 256 / stride;  // distinct states of the quad
     float M = -INFINITY;
-    for (int k = 0; k < groups; ++k) M = fmaxf(M, pm[t + k * quads]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (k < count) M = fmaxf(M, pm[t + k * stride]);
     float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
     float L = 0.f;
-    for (int k = 0; k < groups; ++k) {
-      const float mk = pm[t + k * quads];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (k >= count) break;
+      const float mk = pm[t + k * stride];
       const float f = mk == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mk - M);
-      const float4 o = part[t + k * quads];
+      const float4 o = part[t + k * stride];
       s4.x = fmaf(o.x, f, s4.x);
       s4.y = fmaf(o.y, f, s4.y);
       s4.z = fmaf(o.z, f, s4.z);
       s4.w = fmaf(o.w, f, s4.w);
-      L = fmaf(pl[t + k * quads], f, L);
+      L = fmaf(pl[t + k * stride], f, L);
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
     row[0][4 * t + 0] = s4.x * inv;
