@@ -625,3 +625,7 @@ def test_prefill_sequence_reference_signature(device):
     K, V = O.dequant_f64(v, np.arange(-(-n // 16)), n)
     ref = O.attention_f64(O.bf16_bits_to_f32(q), K, V, n, 0.05)
     assert O.relerr(to_f32(o), ref) < 5e-3
+    # the reference's undispatched single-kernel variant (int4_prefill.py:176-200) has the same contract
+    o8 = int4_prefill.prefill_sequence_i8(bf16_tensor(q, device), kc, vc, ks, vs,
+                                          torch.arange(-(-n // 16), dtype=torch.int32, device=device), n, 0.05)
+    assert o8.dtype == torch.bfloat16 and O.relerr(to_f32(o8), ref) < 5e-3
