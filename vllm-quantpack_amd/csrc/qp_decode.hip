@@ -490,6 +490,93 @@ __device__ __forceinline__ void finish_workgroup(WaveState<HS, KFMT, NCT> &st, u
   }
 }
 
+// The same merge without waiting for the slowest wave before parking: every wave parks its unscaled rows (acc - c) in
+// its own stage buffers (REGION bytes from smem + w * REGION, free once its last chunk is read) as soon as its loop
+// ends, while the other waves still run; after one barrier all threads sum the parked rows with the factors
+// 2^(m_w - M). Only valid rows are parked. st_m / st_l: WAVES * NCT * 16 floats each, outside the stage buffers.
+template <int HS, int KFMT, int NCT, int WAVES, int REGION>
+__device__ __forceinline__ void finish_workgroup_own(WaveState<HS, KFMT, NCT> &st, uint8_t *smem, float *st_m,
+                                                     float *st_l, const DecodeParams &p, int w, int col, int g,
+                                                     int q0, int T, int G, int h, int seg_idx) {
+  constexpr int kORow = HS + 4;
+  constexpr int kRows = NCT * 16;
+  static_assert(kRows * kORow * 4 <= REGION, "a wave's stage buffers hold its parked rows");
+  const int R = T * G;
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    st.l[ct] = rows_sum(st.l[ct]);
+    st.c[ct] = rows_sum(st.c[ct]);
+  }
+  if (g == 0) {
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      st_m[w * kRows + ct * 16 + col] = st.m[ct];
+      st_l[w * kRows + ct * 16 + col] = st.l[ct];
+    }
+  }
+  float *own = reinterpret_cast<float *>(smem + w * REGION);
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    const int r = ct * 16 + col;
+    if (r < R) {
+      const float cr = st.c[ct];
+      float *orow = own + r * kORow;
+#pragma unroll
+      for (int b = 0; b < HS / 64; ++b)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float4 v;
+          v.x = st.acc[ct][b * 4 + 0][j] - cr;
+          v.y = st.acc[ct][b * 4 + 1][j] - cr;
+          v.z = st.acc[ct][b * 4 + 2][j] - cr;
+          v.w = st.acc[ct][b * 4 + 3][j] - cr;
+          *reinterpret_cast<float4 *>(orow + 64 * b + 16 * g + 4 * j) = v;
+        }
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < R * (HS / 4); idx += WAVES * 64) {
+    const int r = idx / (HS / 4), c4 = idx % (HS / 4);
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < WAVES; ++ww) M = fmaxf(M, st_m[ww * kRows + r]);
+    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int ww = 0; ww < WAVES; ++ww) {
+      const float mw = st_m[ww * kRows + r];
+      const float f = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+      const float4 v = reinterpret_cast<const float4 *>(smem + ww * REGION)[r * (kORow / 4) + c4];
+      sum.x = fmaf(v.x, f, sum.x);
+      sum.y = fmaf(v.y, f, sum.y);
+      sum.z = fmaf(v.z, f, sum.z);
+      sum.w = fmaf(v.w, f, sum.w);
+    }
+    const int t = r / G, j = r % G;
+    float *dst = p.so + (int64_t)(q0 + t) * p.sos0 + (int64_t)(h * G + j) * p.sos1 + (int64_t)seg_idx * p.sos2;
+    reinterpret_cast<float4 *>(dst)[c4] = sum;
+  }
+  if (w == 0 && g == 0) {
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      const int r = ct * 16 + col;
+      if (r < R) {
+        float M = -INFINITY, L = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < WAVES; ++ww) M = fmaxf(M, st_m[ww * kRows + r]);
+#pragma unroll
+        for (int ww = 0; ww < WAVES; ++ww) {
+          const float mw = st_m[ww * kRows + r];
+          if (mw != -INFINITY) L += st_l[ww * kRows + r] * __builtin_amdgcn_exp2f(mw - M);
+        }
+        const int t = r / G, j = r % G;
+        const int64_t o = (int64_t)(q0 + t) * p.sts0 + (int64_t)(h * G + j) * p.sts1 + seg_idx;
+        p.smax[o] = M;
+        p.ssum[o] = L;
+      }
+    }
+  }
+}
+
 template <int HS, int NCT, int WAVES>
 constexpr int merge_lds_bytes() {
   return 2 * WAVES * NCT * 16 * 4 + WAVES * NCT * 16 * (HS + 4) * 4;
@@ -772,6 +859,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
   // scalar stores from the in-flight copies and does not wait for the copies before them
   __shared__ __attribute__((aligned(16))) uint8_t smem[kLds];
   __shared__ __attribute__((aligned(16))) float4 kfl[WAVES][kStages][kChunk];
+  // the merge parks each wave's rows in its own stage buffers where they fit (finish_workgroup_own)
+  constexpr bool kOwnMerge = NCT * 16 * (HS + 4) * 4 <= kStages * 2 * Sh::kHalf;
+  __shared__ float mst[2][kOwnMerge ? WAVES * NCT * 16 : 1];
   __shared__ f32x4_t rsc[WAVES][acc_in_agprs<HS, KFMT, NCT>() ? 64 : 1];  // rescale of AGPR accumulators
   // Two row tiles of query operands (64 registers at head 256) are read from LDS instead of being held: the wave
   // state then fits the VGPRs without spills. Every wave of the workgroup attends the same rows.
@@ -860,7 +950,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
       if (!step(1)) break;
     }
   }
-  if constexpr (kParMerge) finish_workgroup<HS, KFMT, NCT, WAVES>(st, smem, p, w, col, g, q0, T, G, h, seg_idx);
+  if constexpr (kOwnMerge)
+    finish_workgroup_own<HS, KFMT, NCT, WAVES, kStages * 2 * Sh::kHalf>(st, smem, mst[0], mst[1], p, w, col, g, q0, T,
+                                                                        G, h, seg_idx);
+  else if constexpr (kParMerge) finish_workgroup<HS, KFMT, NCT, WAVES>(st, smem, p, w, col, g, q0, T, G, h, seg_idx);
   else finish_workgroup_serial<HS, KFMT, NCT, WAVES>(st, smem, p, w, col, g, q0, T, G, h, seg_idx);
 }
 
