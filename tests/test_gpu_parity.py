@@ -109,6 +109,42 @@ def test_decode_scores_far_above_the_running_maximum(device, fmt, T):
     assert O.relerr(out, emu) < 1e-2
 
 
+@pytest.mark.parametrize("fmt,segments,lens", [("int4", 8, [8192]), ("int4", 5, [8192]), ("int4", 64, [32768]),
+                                               ("int8", 16, [8192, 32768])])
+def test_decode_counts_every_chunk_once(device, fmt, segments, lens):
+    """Exact key coverage of the split-KV decode. Zero queries make the softmax uniform, and the value codes light
+    channel c % 256 for the keys of 32-key chunk c (code 1 there, 0 elsewhere; zero point 0, scale 1), so every
+    output channel must equal 32 * (chunks on it) / n exactly, launch after launch: a chunk skipped or taken twice
+    (by two waves, or by two segments) moves its channel by a quarter or more, below any tolerance-based test's
+    reach at these lengths. 5 segments leave a partial last segment; the batch covers two sequences at once."""
+    import torch
+    hs, nkv, nq, bs = 256, 2, 4, 16
+    nbs = [n // bs for n in lens]
+    cell = O.int4_cell_bytes(hs) if fmt == "int4" else O.k8v4_cell_bytes(hs)
+    kv = O.new_cache(sum(nbs), nkv, bs, cell, "hnd")
+    v = O.int4_views(kv, hs) if fmt == "int4" else O.k8v4_views(kv, hs)
+    table = np.zeros((len(lens), max(nbs)), np.int32)
+    at = 0
+    for i, (n, nb) in enumerate(zip(lens, nbs)):
+        table[i, :nb] = np.arange(at, at + nb)
+        keys = np.arange(n)
+        ch = (keys // 32) % hs
+        v.value[at + keys // bs, keys % bs, :, ch // 2] = (1 << (4 * (ch % 2))).astype(np.uint8)[:, None]
+        at += nb
+    v.value_word[...] = np.float32(1.0).view(np.uint32)
+    v.key_word[...] = np.float32(1.0).view(np.uint32)
+    _, views = torch_cache(kv, hs, fmt, device)
+    q = torch.zeros((len(lens), nq, hs), dtype=torch.bfloat16, device=device)
+    cu = i32(np.arange(len(lens) + 1), device)
+    expect = np.zeros((len(lens), nq, hs), np.float32)
+    for i, n in enumerate(lens):
+        per = np.bincount((np.arange(n // 32)) % hs, minlength=hs)
+        expect[i] = (32.0 * per / n)[None, :]
+    for _ in range(3):
+        out, _ = run_decode(views, q, cu, i32(lens, device), i32(table, device), 1, hs ** -0.5, segments, device)
+        assert np.array_equal(out, expect), np.abs(out - expect).max()
+
+
 @pytest.mark.parametrize("layout,bs", [("nhd", 16), ("hnd", 32), ("hnd", 3072), ("nhd", 48)])
 def test_decode_layouts_and_block_sizes(device, layout, bs):
     rng = np.random.default_rng(7 + bs)
