@@ -1,7 +1,7 @@
 """Numpy restatement of vllm-quantpack's int4_per_token_head / k8v4_per_token_head KV-cache attention arithmetic.
 
-TEST INFRASTRUCTURE: the checker for the HIP kernels and the CPU baseline of the benchmark. Nothing in the product
-package imports this module.
+TEST INFRASTRUCTURE: the results the tests compare the HIP kernels with, and the CPU baseline of the benchmark.
+Nothing in the product package imports this module.
 
 Every function cites the reference file:line it restates (paths relative to the reference repository root). The
 kernels the plugin edits live in vLLM (`vllm.v1.attention.ops.int4_per_token_head`), which the reference does not
