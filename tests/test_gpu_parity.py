@@ -179,6 +179,23 @@ def test_decode_ragged_batch(device):
         at += T
 
 
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+def test_decode_short_contexts(device, fmt):
+    """Contexts of a few keys: as many keys as query tokens (each token sees only the keys up to itself), one
+    partial 32-key chunk, a chunk and one key, with most of the 16 segments of every sequence empty. 6 query heads
+    per KV head make 24 query rows (two row tiles) at 4 tokens."""
+    rng = np.random.default_rng(71 + (10 if fmt == "int8" else 0))
+    lens = [(1, 1), (2, 2), (4, 4), (3, 17), (1, 33), (4, 31), (2, 47)]
+    out, emu, ref, _ = _decode_case(device, rng, fmt, lens, nq=12, nkv=2, segments=16)
+    assert np.isfinite(out).all()
+    at = 0
+    for T, n in lens:
+        sl = slice(at, at + T)
+        assert O.relerr(out[sl], emu[sl]) < 1e-2, (T, n)
+        assert O.relerr(out[sl], ref[sl]) < 5e-3, (T, n)
+        at += T
+
+
 def test_decode_segment_count_invariance(device):
     rng = np.random.default_rng(31)
     outs = []
