@@ -574,11 +574,12 @@ def test_prefill_fused_rotation(device):
         assert O.relerr(to_f32(got), want) < 1e-2, splits
 
 
-def test_prefill_varlen_batch(device):
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+def test_prefill_varlen_batch(device, fmt):
     """A batch mixing a long chunk, a first chunk (context == chunk), short chunks and single tokens."""
-    rng = np.random.default_rng(202)
+    rng = np.random.default_rng(202 + (10 if fmt == "int8" else 0))
     lens = [(70, 2500), (5, 900), (1, 1), (33, 33), (16, 4000), (17, 64)]
-    out, emu, ref = _prefill_case(device, rng, "int4", lens)
+    out, emu, ref = _prefill_case(device, rng, fmt, lens)
     at = 0
     for T, n in lens:
         sl = slice(at, at + T)
