@@ -236,6 +236,18 @@ def _build_module():
     return mod
 
 
+def test_inline_mfma_sources_are_scanned():
+    """Every source with an inline-assembly MFMA goes through the scan, also when the MFMA is not the first
+    instruction of its assembly string (the decode's PV tiles open with the wait states their operands need)."""
+    build = _build_module()
+    assert build.has_inline_mfma('asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(x));')
+    assert build.has_inline_mfma('asm volatile("s_nop 1\\n\\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(x));')
+    assert not build.has_inline_mfma('asm volatile("s_mov_b32 m0, %1\\n\\ts_nop 0" ::"s"(x));\n// v_mfma in a comment')
+    csrc = os.path.join(os.path.dirname(build.__file__), "csrc")
+    for name in ("qp_decode.hip", "qp_prefill.hip"):
+        assert build.has_inline_mfma(open(os.path.join(csrc, name)).read()), name
+
+
 def test_inline_mfma_wait_scan():
     """The build's scan flags a read of an inline-assembly MFMA result inside the wait window and nothing else."""
     scan = _build_module().mfma_hazards

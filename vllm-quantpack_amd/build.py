@@ -109,9 +109,14 @@ def mfma_hazards(asm):
     return found
 
 
+def has_inline_mfma(text):
+    """Whether a source holds an inline-assembly MFMA, wherever it stands in its assembly string."""
+    return re.search(r'asm\s+volatile\s*\(\s*"[^;]*?v_mfma', text) is not None
+
+
 def _check_inline_mfma(src, verbose):
     text = open(src).read()
-    if not re.search(r'asm\s+volatile\s*\(\s*"[^;]*?v_mfma', text):
+    if not has_inline_mfma(text):
         return
     out = os.path.join(OBJ, os.path.basename(src).replace(".hip", ".gfx.s"))
     cmd = [hipcc(), *_flags(src), "--cuda-device-only", "-S", src, "-o", out]
