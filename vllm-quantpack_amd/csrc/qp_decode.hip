@@ -10,10 +10,14 @@
 // MI355X design (one workgroup of W waves per (segment, KV head, sequence)):
 //   * Every query row of the KV head's GQA group (T tokens x G heads, up to 32 rows) sits in one workgroup, so the
 //     segment's cache bytes are read from HBM once per step.
-//   * Each wave streams its own 32-key chunks (chunk w, w + W, ...) into wave-private LDS. For the standard HND
-//     cache (each (block, KV head) page span of 16 cells contiguous) the span bytes go straight from HBM to LDS with
-//     global_load_lds_dwordx4 (no VGPR staging), double-buffered, waits placed by hand; any other strided layout
-//     goes through VGPR buffer loads into padded LDS rows.
+//   * Each wave streams 32-key chunks into wave-private LDS stages: its first ones statically (chunk w, w + W, ...),
+//     the rest from a workgroup counter as stages free up. For the standard HND cache (each (block, KV head) page
+//     span of 16 cells contiguous) the span bytes go straight from HBM to LDS with global_load_lds_dwordx4 (no VGPR
+//     staging), in one or two stages per wave, waits placed by hand; any other strided layout goes through VGPR
+//     buffer loads into padded LDS rows.
+//   * 8 waves (two per SIMD) for one row tile up to head 256; 4 waves for two row tiles (their O^T accumulators in
+//     AGPRs through inline-assembly MFMAs, the query operands read from LDS) and for head 512, where more than 16
+//     rows run as workgroups of whole tokens.
 //   * QK^T runs as S^T = K Q^T on v_mfma_f32_16x16x32_bf16 with the K tile as the A operand: nibbles become exact
 //     bf16 integers 128 + n (one v_bitop3 per pair plus shifts), the Q operand is permuted to match. The S^T
 //     accumulator layout (4 keys x 1 query row per lane) is exactly the B operand layout of O^T = V^T P^T, so P
@@ -22,8 +26,9 @@
 //     needs.
 //   * The +128 offsets are removed through per-key scalars: S uses (128 + zp_k) * sum(q); the output subtracts
 //     sum(P_v16 * (128 + zp_v)), accumulated from the same rounded P_v16 that feeds the MFMA.
-//   * Online softmax in base 2 with a lazy rescale (only when a row maximum grows); the waves' states merge in LDS
-//     at the end and the workgroup writes one (acc, m, l) partial per row.
+//   * Online softmax in base 2 with a lazy rescale (only when a row maximum grows by more than 2^8); the waves'
+//     states merge in LDS at the end (each wave parking its rows in its own stage buffers where they fit) and the
+//     workgroup writes one (acc, m, l) partial per row.
 #include "qp_common.h"
 
 namespace qp {
