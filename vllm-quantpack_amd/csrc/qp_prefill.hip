@@ -415,7 +415,9 @@ __device__ __forceinline__ void pf_initial_max(PfRows<HS, NT> &r, const f32x4_t 
 //   phase A: S^T of tile i + 1 (K from kd1; 3 MFMAs per K operand, one per row tile)
 //            + softmax of tile i (scores sprev, scalars from vb0) + the K part of tile i + 2's unpack;
 //   phase B: O^T += V^T P^T of tile i (V^T from vb0) + the V part of tile i + 2's unpack.
-// Each phase is a sequence of MFMA steps fenced by sched_barrier, the operand loads running a fixed distance ahead.
+// Each phase is written as a sequence of MFMA steps, the operand loads three steps ahead and the VALU work spread
+// between them. The steps are not fenced: the compiler's own interleaving across steps measures 5 % faster than
+// sched_barrier fences after every step (4.09-4.15 against 4.37 ms on the 1024-token chunk over 131072 keys).
 // A score beyond the headroom only posts a restart request (the tile index) for the next barrier.
 template <int HS, int KFMT, int NT, bool MASK>
 __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev)[NT][2], f32x4_t (&snew)[NT][2],
@@ -495,7 +497,6 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
       const int at = 1 + q * (kQ - 1) / (NT * kSm);
       if (s == at) sm_item(q / kSm, q % kSm);
     }
-    __builtin_amdgcn_sched_barrier(0);
   }
 
   // ---- phase B
@@ -518,7 +519,6 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       if (at(b, c + 8)) st.v_store(c);
-    __builtin_amdgcn_sched_barrier(0);
   }
 
   if (__builtin_expect(trig && may_restart, 0)) {
