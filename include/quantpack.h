@@ -90,6 +90,8 @@ typedef struct qp_decode_args {
   float *segm_expsum;          /* fp32 [rows, num_q_heads, S]: sum_j 2^(s_j - segm_max) */
   int64_t segm_stat_stride[2]; /* elements: row, head (segments contiguous) */
   int32_t segm_rows;           /* rows of the segment buffers: num_tokens must not exceed it */
+  const float *query_signs;    /* optional: q is unrotated; each row is rotated to (q D) H (D = these +/-1 signs, H
+                                  Sylvester) and rounded to bf16 as it loads, bit-identical to qp_rht then decode */
 } qp_decode_args;
 
 int qp_decode_splitkv(const qp_paged_cache *cache, const qp_decode_args *args, qp_stream_t stream);
@@ -158,12 +160,61 @@ typedef struct qp_prefill_args {
   int64_t workspace_bytes;
   const float *rht_signs;      /* optional: inverse rotation of the output (needs a contiguous out) */
   float rht_out_scale;
+  const float *query_signs;    /* optional: q is unrotated and rotated on load, as in qp_decode_args */
 } qp_prefill_args;
 
 int qp_prefill(const qp_paged_cache *cache, const qp_prefill_args *args, qp_stream_t stream);
 
 /* Workspace bytes qp_prefill uses for these arguments on the current device (0 when it does not split). */
 int64_t qp_prefill_workspace_size(const qp_paged_cache *cache, const qp_prefill_args *args);
+
+/*
+ * One attention step of a batch over the paged cache, routed on the device with no host synchronisation:
+ *   - every sequence with 1..QP_DECODE_MAX_QUERY query tokens whose rows fit the segment buffers goes to the split-KV
+ *     decode (one workgroup per segment holding the GQA group's rows) and the log-sum-exp merge;
+ *   - every other sequence (prefill chunks) goes to the MFMA prefill kernel, or its query-slice path.
+ * A batch of short sequences only (max_query_len <= QP_DECODE_MAX_QUERY, num_tokens <= segm_rows) is decode + merge
+ * with partial rows at the tokens' own indices and needs no workspace, so it can be recorded in a HIP graph. A mixed
+ * batch packs its short sequences' rows into the segment buffers through a route table in the workspace. With
+ * rht_signs, q is unrotated (rotated to (q D) H as it loads) and the output is rotated back, (o H D) * rht_out_scale,
+ * inside the kernels: the call is the whole of unified_attention_int4.
+ * Replaces the stock unified_attention_int4 with the reference's router around it (int4_kv.py:294-329: the decode /
+ * MTP rows as a split-KV sub-batch, long chunks to the prefill path, single_rht before and after, :307-329).
+ */
+typedef struct qp_attention_args {
+  const void *query;           /* bf16 [num_tokens, num_q_heads, head_size] */
+  int64_t query_stride[2];     /* elements: token, head; channels contiguous */
+  const int32_t *cu_seqlens_q; /* [num_seqs + 1] */
+  const int32_t *seqused_k;    /* [num_seqs] */
+  const int32_t *block_table;
+  int64_t block_table_stride;
+  int32_t num_seqs;
+  int32_t num_tokens;
+  int32_t num_q_heads;
+  int32_t max_query_len;
+  int32_t max_seqlen_k;        /* longest context (bounds the prefill's automatic key splits) */
+  float softmax_scale;         /* multiplies q.k in the cache's domain */
+  void *out;                   /* bf16 [num_tokens, num_q_heads, head_size], contiguous when rht_signs is set */
+  int64_t out_stride[2];
+  float *segm_output;          /* split-KV segment buffers as in qp_decode_args; NULL: everything takes the prefill */
+  int64_t segm_output_stride[3];
+  float *segm_max;
+  float *segm_expsum;
+  int64_t segm_stat_stride[2];
+  int32_t segm_rows;
+  int32_t num_segments;
+  int32_t max_decode_rows;     /* query rows (tokens x GQA heads) one split-KV workgroup may hold: 16 or 32 (0 = 32);
+                                  above it a sequence's tokens are served in groups that each read the segment */
+  const float *rht_signs;      /* optional: rotate q on load and the output back */
+  float rht_out_scale;
+  void *workspace;             /* >= qp_attention_workspace_size bytes, 256-byte aligned (NULL when that is 0) */
+  int64_t workspace_bytes;
+} qp_attention_args;
+
+int qp_attention(const qp_paged_cache *cache, const qp_attention_args *args, qp_stream_t stream);
+
+/* Workspace bytes qp_attention uses for these arguments on the current device (0 for a batch of short sequences). */
+int64_t qp_attention_workspace_size(const qp_paged_cache *cache, const qp_attention_args *args);
 
 /*
  * Quantise-and-store of new keys/values into the paged cache: per (token, KV head) keys to int4 (asymmetric

@@ -9,8 +9,10 @@ vendor; where a detail comes from vLLM and not from the plugin's own text, the d
 
 Pinning (the checks that tie each function to something other than its own formula) is done in
 tests/test_oracle_pinning.py; the table there names, per function, the known answers, closed forms and planted
-mistakes used. Functions with no such check would say "parity unpinned" here; at present every function below is
-pinned by at least one of them, with the bit-level limits stated in its docstring.
+mistakes used. Every function below is pinned by at least one of them. Parity unpinned at bit level, and said so in
+the docstrings concerned: the fused multiply-add assumed in the int4 store's `v * inv + zp` (`_fma32`), vLLM's own
+RHT sign vector (`rht_signs`), and the int4 store's key half (inferred equal to its value half). Those are pinned only
+to tolerance, through the fp64 closed form.
 """
 from __future__ import annotations
 
@@ -218,7 +220,27 @@ def relerr(o, ref) -> float:
     return float(np.linalg.norm(o - ref) / np.linalg.norm(ref))
 
 
+def max_row_relerr(o, ref) -> float:
+    """Largest relative error of one output row (the head_size vector of one (token, head)):
+    max_r ||o_r - ref_r|| / ||ref_r||. A stricter reading of "max relative error" than the Frobenius figure of the
+    reference's own test, which a few bad rows among many cannot hide in."""
+    o = np.asarray(o, np.float64)
+    ref = np.asarray(ref, np.float64)
+    hs = ref.shape[-1]
+    num = np.linalg.norm((o - ref).reshape(-1, hs), axis=1)
+    den = np.linalg.norm(ref.reshape(-1, hs), axis=1)
+    return float((num / np.where(den > 0, den, 1.0)).max())
+
+
 # ------------------------------------------------------------------------- exact read kernel emulation (a7-a9)
+
+def value_probabilities(P: np.ndarray, s_v: np.ndarray, zp_v: np.ndarray):
+    """(P_v16, zero-point sum) of one tile: P_v16 = bf16(P * s_v) is the PV operand, and the zero-point correction
+    sum_j fp32(P_v16_j) * zp_v_j is taken on that same rounded P_v16, not on the fp32 P * s_v (int4_kv.py:90-94:
+    `P_v16 = P_v.to(...)`, `Pv_zp_sum = tl.sum(P_v16.to(tl.float32) * v_zp[None, :], axis=1)`). P [rows, keys]."""
+    P16 = round_bf16(P * s_v[None, :])
+    return P16, (P16 * zp_v[None, :]).sum(axis=1, dtype=np.float32)
+
 
 def segment_length(n: int, num_segments: int, tile: int) -> int:
     """Keys per split-KV segment: `cdiv(n, S * tile) * tile` (the 3D kernel's tiles_per_segment; inferred from
@@ -283,8 +305,7 @@ def decode_partials(q: np.ndarray, views: CacheViews, block_row, n: int, scale: 
                 l = l * alpha + P.sum(axis=1, dtype=np.float32)
                 m = m_new
                 zp_v, s_v = int4_word_parts(vw)
-                P16 = round_bf16(P * s_v[None, :])
-                corr = (P16 * zp_v[None, :]).sum(axis=1, dtype=np.float32)
+                P16, corr = value_probabilities(P, s_v, zp_v)
                 a_even = a_even * alpha[:, None] + (P16 @ (vc & 0xF).astype(np.float32)) - corr[:, None]
                 a_odd = a_odd * alpha[:, None] + (P16 @ ((vc >> 4) & 0xF).astype(np.float32)) - corr[:, None]
             out = np.empty((T * g, hs), np.float32)
@@ -309,9 +330,29 @@ def merge_partials(acc: np.ndarray, m: np.ndarray, l: np.ndarray) -> np.ndarray:
 
 
 def segment_lse(m: np.ndarray, l: np.ndarray) -> np.ndarray:
-    """Natural-log LSE of a segment from (m in log2 units, l): (m + log2 l) * ln 2; -inf for an empty one."""
+    """Natural-log LSE of a segment from (m in log2 units, l): (m + log2 l) * ln 2; -inf for an empty one
+    (m = -inf, l = 0). The per-segment LSE the split-KV path carries, in the natural-log units of the `lse` that
+    int4_prefill.py:223-230 folds with `logaddexp`."""
+    m = np.asarray(m, np.float64)
+    l = np.asarray(l, np.float64)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        out = (m + np.log2(l)) * math.log(2)
+    return np.where((l > 0) & np.isfinite(m), out, -np.inf).astype(np.float32)
+
+
+def merge_lse(m: np.ndarray, l: np.ndarray) -> np.ndarray:
+    """Natural-log LSE of whole rows from their segments' statistics (last axis = segment): ln sum_s l_s 2^(m_s),
+    the `logaddexp` fold of int4_prefill.py:223-230 over the segments. -inf when every segment is empty."""
+    m = np.asarray(m, np.float64)
+    l = np.asarray(l, np.float64)
+    M = m.max(axis=-1)
+    Ms = np.where(np.isfinite(M), M, 0.0)
+    with np.errstate(invalid="ignore"):
+        w = np.where(np.isfinite(m), np.exp2(m - Ms[..., None]), 0.0)
+    L = (l * w).sum(axis=-1)
     with np.errstate(divide="ignore"):
-        return ((m.astype(np.float64) + np.log2(l.astype(np.float64))) * math.log(2)).astype(np.float32)
+        out = (Ms + np.log2(L)) * math.log(2)
+    return np.where(L > 0, out, -np.inf).astype(np.float32)
 
 
 def decode_emulated(q, views, block_row, n, scale, num_segments=1, tile=64) -> np.ndarray:
@@ -390,7 +431,10 @@ def round_half_away(x: np.ndarray) -> np.ndarray:
 
 def _fma32(a, b, c) -> np.ndarray:
     """fp32 fused multiply-add: the fp64 product of two fp32 values plus a small integer is exact, so one rounding
-    to fp32 gives the correctly rounded result (Triton contracts `a * b + c`, k8v4_ops.py:454-455)."""
+    to fp32 gives the correctly rounded result. Used for `v * inv_v + v_zp` (k8v4_ops.py:55-56) on the assumption
+    that Triton contracts it into one FMA (its `enable_fp_fusion` compile option is on by default). Parity unpinned:
+    Triton cannot run here, and the reference holds no stored codes that would show which of the two it does; a
+    mul-then-add store differs from this one in the codes of a few channels near a rounding boundary."""
     return (np.asarray(a, np.float64) * np.asarray(b, np.float64) + np.asarray(c, np.float64)).astype(np.float32)
 
 

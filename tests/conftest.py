@@ -27,3 +27,12 @@ def device():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     return torch.device("cuda:0")
+
+
+@pytest.fixture(autouse=True)
+def _restore_vllm_hooks():
+    """Hooks a test installs into stand-in vLLM objects are undone after it."""
+    yield
+    hooks = sys.modules.get("vllm_quantpack.attention.vllm_hooks")
+    if hooks is not None:
+        hooks.HOOKS.restore()

@@ -5,6 +5,14 @@ import numpy as np
 from oracle import qp_oracle as O
 
 
+def assert_emulation(out, emu, what=None):
+    """The bar against the oracle's emulation of the reference's exact kernel: relative error below 1e-2 as the
+    reference's own test measures it (Frobenius over the output, tests/test_int4_kv.py:160-161,190) and for every
+    (token, head) output row on its own."""
+    fro, row = O.relerr(out, emu), O.max_row_relerr(out, emu)
+    assert fro < 1e-2 and row < 1e-2, (what, f"frobenius {fro:.3e}, worst row {row:.3e}")
+
+
 def word(scale, zp):
     return np.uint32((int(np.float32(scale).view(np.uint32)) & 0xFFFFFFF0) | int(zp))
 

@@ -1,14 +1,16 @@
 """Parity of the HIP kernels with the CPU oracle, on seeded inputs (runs on the MI355X through the C ABI).
 
-Bars: the unpack and the store are bit-exact; attention is within 1e-2 relative (Frobenius, the reference's own test
-metric, tests/test_int4_kv.py:160-161,190) of the oracle's emulation of the reference's exact kernel, and within
-0.5 % of the fp64 closed form.
+Bars: the unpack and the store are bit-exact; attention is within 1e-2 relative of the oracle's emulation of the
+reference's exact kernel, both as the reference's own test metric (Frobenius over the whole output,
+tests/test_int4_kv.py:160-161,190) and row by row (the largest error of any (token, head) output vector), and within
+0.5 % (Frobenius) of the fp64 closed form.
 """
 import numpy as np
 import pytest
 
 from oracle import qp_oracle as O
-from qp_testlib import bf16_tensor, i32, random_cache, run_decode, to_f32, torch_cache
+from test_oracle_pinning import fma_rows
+from qp_testlib import assert_emulation, bf16_tensor, i32, random_cache, run_decode, to_f32, torch_cache
 
 pytestmark = pytest.mark.gpu
 
@@ -89,7 +91,7 @@ def _decode_case(device, rng, fmt, lens, layout="hnd", bs=16, segments=8, nq=NQ,
 def test_decode_matches_oracle(device, fmt, T):
     rng = np.random.default_rng(100 + T + (10 if fmt == "int8" else 0))
     out, emu, ref, _ = _decode_case(device, rng, fmt, [(T, 5003)], segments=7)
-    assert O.relerr(out, emu) < 1e-2
+    assert_emulation(out, emu)
     assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
 
 
@@ -106,7 +108,7 @@ def test_decode_scores_far_above_the_running_maximum(device, fmt, T):
                                     big_keys=[(1504, 16, f1), (2900, 8, f2)])
     assert np.isfinite(out).all()
     assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
-    assert O.relerr(out, emu) < 1e-2
+    assert_emulation(out, emu)
 
 
 @pytest.mark.parametrize("fmt,segments,lens", [("int4", 8, [8192]), ("int4", 5, [8192]), ("int4", 64, [32768]),
@@ -149,7 +151,7 @@ def test_decode_counts_every_chunk_once(device, fmt, segments, lens):
 def test_decode_layouts_and_block_sizes(device, layout, bs):
     rng = np.random.default_rng(7 + bs)
     out, emu, ref, _ = _decode_case(device, rng, "int4", [(2, 4100)], layout=layout, bs=bs, segments=5)
-    assert O.relerr(out, emu) < 1e-2
+    assert_emulation(out, emu)
     assert O.relerr(out, ref) < 5e-3
 
 
@@ -160,7 +162,8 @@ def test_decode_span_and_row_loaders_agree(device, fmt, T, monkeypatch):
     a, emu, ref, _ = _decode_case(device, np.random.default_rng(5), fmt, [(T, 3000), (1, 200)], segments=9)
     monkeypatch.setenv("QP_DECODE_ROWS", "1")
     b, _, _, _ = _decode_case(device, np.random.default_rng(5), fmt, [(T, 3000), (1, 200)], segments=9)
-    assert O.relerr(a, emu) < 1e-2 and O.relerr(b, emu) < 1e-2
+    assert_emulation(a, emu)
+    assert_emulation(b, emu)
     assert O.relerr(a, ref) < 5e-3 and O.relerr(b, ref) < 5e-3
     assert O.relerr(a, b) < 5e-3
 
@@ -174,7 +177,7 @@ def test_decode_ragged_batch(device):
     at = 0
     for T, n in lens:
         sl = slice(at, at + T)
-        assert O.relerr(out[sl], emu[sl]) < 1e-2, (T, n)
+        assert_emulation(out[sl], emu[sl], (T, n))
         assert O.relerr(out[sl], ref[sl]) < 5e-3, (T, n)
         at += T
 
@@ -191,7 +194,7 @@ def test_decode_short_contexts(device, fmt):
     at = 0
     for T, n in lens:
         sl = slice(at, at + T)
-        assert O.relerr(out[sl], emu[sl]) < 1e-2, (T, n)
+        assert_emulation(out[sl], emu[sl], (T, n))
         assert O.relerr(out[sl], ref[sl]) < 5e-3, (T, n)
         at += T
 
@@ -221,6 +224,92 @@ def test_decode_partials_match_the_emulation(device):
     f = np.exp2(gm - m[:, :, :active])
     assert np.allclose(gl * f, l_[:, :, :active], rtol=1e-3)
     assert O.relerr(go * f[..., None], acc[:, :, :active]) < 1e-2
+
+
+@pytest.mark.parametrize("fmt,lens,segments", [("int4", [(2, 4096)], 64), ("int4", [(1, 900)], 8),
+                                                ("int8", [(1, 2100), (2, 5000), (1, 3000), (2, 2048)], 16)],
+                         ids=["mtp1-4096", "decode-900", "k8v4-ragged"])
+def test_merge_lse_matches_the_oracle(device, fmt, lens, segments):
+    """The merge's optional lse output (natural log, per token and query head) against the oracle's fold of the
+    emulated segment statistics and against the fp64 logsumexp of the scores over the visible keys: the per-row
+    log-sum-exp a caller folds with other partial attentions (the `logaddexp` merge of int4_prefill.py:223-230)."""
+    import torch
+    from scipy.special import logsumexp
+
+    from vllm_quantpack.attention import int4_kv
+    rng = np.random.default_rng(sum(t * n for t, n in lens) % 1000)
+    _, _, _, ctx = _decode_case(device, rng, fmt, lens, segments=segments)
+    so, sm, ss = ctx["bufs"]
+    Ts = [t for t, _ in lens]
+    cu = np.concatenate(([0], np.cumsum(Ts))).astype(np.int32)
+    lse = torch.full((sum(Ts), NQ), float("nan"), dtype=torch.float32, device=device)
+    out = torch.empty((sum(Ts), NQ, HS), dtype=torch.bfloat16, device=device)
+    margs = int4_kv._hip.MergeArgs(so.data_ptr(), int4_kv._hip.I64x3(*so.stride()[:3]), sm.data_ptr(),
+                                   ss.data_ptr(), int4_kv._hip.I64x2(sm.stride(0), sm.stride(1)),
+                                   i32(cu, device).data_ptr(), i32([n for _, n in lens], device).data_ptr(),
+                                   len(lens), sum(Ts), NQ, HS, segments, out.data_ptr(),
+                                   int4_kv._hip.I64x2(out.stride(0), out.stride(1)), lse.data_ptr(),
+                                   int4_kv._hip.I64x2(lse.stride(0), lse.stride(1)), None, 1.0)
+    keep = (cu, lens)
+    int4_kv._hip.check(int4_kv._hip.lib().qp_merge_segments(margs, int4_kv._hip.stream_of(out)), "merge")
+    torch.cuda.synchronize()
+    del keep
+    got = to_f32(lse)
+    scale = HS ** -0.5
+    for i, (T, n) in enumerate(lens):
+        qs = ctx["q"][cu[i]:cu[i + 1]]
+        _, m, l_ = O.decode_partials(qs, ctx["views"], ctx["table"][i], n, scale, segments, tile=32)
+        want = O.merge_lse(m, l_)
+        assert np.abs(got[cu[i]:cu[i + 1]] - want).max() < 1e-4, i
+        K, _ = O.dequant_f64(ctx["views"], ctx["table"][i], n)
+        for t in range(T):
+            vis = n - T + t + 1
+            for h in range(0, NQ, 5):
+                ref = logsumexp(scale * (K[:vis, h // (NQ // NKV)] @ qs[t, h].astype(np.float64)))
+                assert abs(got[cu[i] + t, h] - ref) < 1e-4, (i, t, h)
+
+
+def _dead_value_cache(rng, fmt, n, bs=16, live=2):
+    """A cache whose value codes equal their zero points (value 0) on all keys but `live` ones."""
+    nb = -(-n // bs)
+    kv, v = random_cache(rng, nb, NKV, bs, HS, fmt)
+    zp = (v.value_word & np.uint32(0xF)).astype(np.uint8)
+    v.value[...] = zp[..., None] | (zp[..., None] << 4)
+    for pos in rng.choice(n, live, replace=False):
+        v.value[pos // bs, pos % bs] = rng.integers(0, 256, v.value.shape[-1:], dtype=np.uint8)
+    return kv, v, np.arange(nb, dtype=np.int32)
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+def test_zero_point_sum_uses_the_rounded_probabilities(device, fmt):
+    """int4_kv.py:90-94 through both kernels: the zero-point correction sum_j P16_j zp_j must come from the same
+    bf16-rounded P16 = bf16(P s_v) that the PV product takes. With values at their zero points on all keys but two,
+    the true output is small and a sum on the unrounded P s_v misses fp64 by 3-28 % (the oracle's planted variant);
+    both the decode and the prefill kernel stay within the usual bar."""
+    import torch
+
+    from vllm_quantpack.attention import int4_prefill
+    rng = np.random.default_rng(95 + (1 if fmt == "int8" else 0))
+    n = 3000
+    kv, v, table = _dead_value_cache(rng, fmt, n)
+    _, (kc, vc, ks, vs) = torch_cache(kv, HS, fmt, device)
+    for T in (2, 64):
+        q = O.f32_to_bf16_bits(rng.standard_normal((T, NQ, HS)).astype(np.float32))
+        qf = O.bf16_bits_to_f32(q)
+        K, V = O.dequant_f64(v, table, n)
+        ref = O.attention_f64(qf, K, V, n, HS ** -0.5)
+        if T <= 4:
+            out, _ = run_decode((kc, vc, ks, vs), bf16_tensor(q, device), i32([0, T], device), i32([n], device),
+                                i32(table[None], device), T, HS ** -0.5, 16, device)
+        else:
+            o = torch.empty((T, NQ, HS), dtype=torch.bfloat16, device=device)
+            int4_prefill.prefill_attention(bf16_tensor(q, device), kc, vc, ks, vs, o,
+                                           cu_seqlens_q=i32([0, T], device), seqused_k=i32([n], device),
+                                           block_table=i32(table[None], device), max_seqlen_q=T,
+                                           softmax_scale=HS ** -0.5)
+            torch.cuda.synchronize()
+            out = to_f32(o)
+        assert O.relerr(out, ref) < 5e-3, (T, O.relerr(out, ref))
 
 
 def test_decode_plan_graph_replays(device):
@@ -279,7 +368,7 @@ def test_decode_head_512(device, fmt, T):
     (one row tile each), the last group of 3 tokens holding a single token."""
     rng = np.random.default_rng(300 + T + (10 if fmt == "int8" else 0))
     out, emu, ref, _ = _decode_case(device, rng, fmt, [(T, 3000), (1, 900)], nq=16, nkv=2, hs=512, segments=6)
-    assert O.relerr(out, emu) < 1e-2
+    assert_emulation(out, emu)
     assert O.relerr(out, ref) < 5e-3
 
 
@@ -289,7 +378,7 @@ def test_decode_gqa_8_and_head_128(device, fmt):
     (8 waves; one stage each with int8 keys)."""
     rng = np.random.default_rng(51 + (10 if fmt == "int8" else 0))
     out, emu, ref, _ = _decode_case(device, rng, fmt, [(4, 2500), (1, 700)], nq=16, nkv=2, hs=128, segments=9)
-    assert O.relerr(out, emu) < 1e-2
+    assert_emulation(out, emu)
     assert O.relerr(out, ref) < 5e-3
 
 
@@ -307,6 +396,11 @@ def test_store_bit_exact(device, fmt, layout):
     t, (kc, vc, ks, vs) = torch_cache(kv_np, HS, fmt, device)
     key = O.f32_to_bf16_bits(rng.standard_normal((n, NKV, HS)).astype(np.float32) * 2)
     val = O.f32_to_bf16_bits(rng.standard_normal((n, NKV, HS)).astype(np.float32))
+    # rows whose probe channel rounds differently under a fused multiply-add and a mul-then-add (int4 halves)
+    rows, _ = fma_rows(HS)
+    val[1:1 + len(rows), 0] = O.f32_to_bf16_bits(rows)
+    if fmt == "int4":
+        key[1:1 + len(rows), 1] = O.f32_to_bf16_bits(rows)
     slots = rng.permutation(nb * bs)[:n].astype(np.int64)
     slots[::17] = -1
     k8v4_kv.store(None, bf16_tensor(key, device), bf16_tensor(val, device), kc, vc,
@@ -361,7 +455,7 @@ def test_rht_matches_fp64_and_inverts(device):
 @pytest.mark.parametrize("fmt", ["int4", "int8"])
 @pytest.mark.parametrize("qlen", [1, 2, 4])
 def test_unified_attention_decode_matches_fp64(device, fmt, qlen):
-    """The reference's end-to-end check (tests/test_int4_kv.py:172-191 / test_k8v4_kv.py:506-520): random bf16 K/V
+    """The reference's end-to-end check (tests/test_int4_kv.py:172-191 / tests/test_k8v4_kv.py:159-173): random bf16 K/V
     stored through reshape_and_cache_int4, attention of unrotated queries against fp64, error < 1e-2 (and < 0.5 %)."""
     import torch
 
@@ -519,7 +613,7 @@ def test_prefill_matches_oracle(device, fmt, layout):
     rng = np.random.default_rng(201)
     out, emu, ref = _prefill_case(device, rng, fmt, [(100, 3000)], layout=layout)
     assert np.isfinite(out).all()
-    assert O.relerr(out, emu) < 1e-2
+    assert_emulation(out, emu)
     assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
 
 
@@ -531,7 +625,7 @@ def test_prefill_key_splits_agree(device, splits):
     lens = [(48, 2600), (7, 300), (33, 33)]
     out, emu, ref = _prefill_case(device, rng, "int4", lens, splits=splits)
     assert np.isfinite(out).all()
-    assert O.relerr(out, emu) < 1e-2
+    assert_emulation(out, emu)
     assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
 
 
@@ -583,7 +677,7 @@ def test_prefill_varlen_batch(device, fmt):
     at = 0
     for T, n in lens:
         sl = slice(at, at + T)
-        assert O.relerr(out[sl], emu[sl]) < 1e-2, (T, n)
+        assert_emulation(out[sl], emu[sl], (T, n))
         assert O.relerr(out[sl], ref[sl]) < 5e-3, (T, n)
         at += T
 
@@ -592,7 +686,7 @@ def test_prefill_varlen_batch(device, fmt):
 def test_prefill_block_sizes_and_gqa(device, bs):
     rng = np.random.default_rng(203 + bs)
     out, emu, ref = _prefill_case(device, rng, "int4", [(40, 2000)], bs=bs, nq=16, nkv=2, hs=128)
-    assert O.relerr(out, emu) < 1e-2
+    assert_emulation(out, emu)
     assert O.relerr(out, ref) < 5e-3
 
 
@@ -602,7 +696,7 @@ def test_prefill_head_512_query_slices(device, fmt):
     these on its Triton kernel: tests/test_int4_kv.py:194-210, tests/test_k8v4_kv.py:208-225). Ragged batch."""
     rng = np.random.default_rng(401 + (1 if fmt == "int8" else 0))
     out, emu, ref = _prefill_case(device, rng, fmt, [(37, 2100), (5, 600), (1, 64)], nq=16, nkv=2, hs=512)
-    assert O.relerr(out, emu) < 1e-2
+    assert_emulation(out, emu)
     assert O.relerr(out, ref) < 5e-3
 
 
@@ -610,7 +704,7 @@ def test_prefill_wide_gqa_query_slices(device):
     """16 query heads per KV head is past the MFMA prefill kernel's 12 and takes the slice path as well."""
     rng = np.random.default_rng(405)
     out, emu, ref = _prefill_case(device, rng, "int4", [(20, 1500), (3, 200)], nq=16, nkv=1, hs=128)
-    assert O.relerr(out, emu) < 1e-2
+    assert_emulation(out, emu)
     assert O.relerr(out, ref) < 5e-3
 
 
@@ -619,7 +713,8 @@ def test_prefill_span_and_row_loaders_agree(device, monkeypatch):
     a, emu, ref = _prefill_case(device, np.random.default_rng(204), "int8", [(64, 1500), (3, 700)])
     monkeypatch.setenv("QP_PREFILL_ROWS", "1")
     b, _, _ = _prefill_case(device, np.random.default_rng(204), "int8", [(64, 1500), (3, 700)])
-    assert O.relerr(a, emu) < 1e-2 and O.relerr(b, emu) < 1e-2
+    assert_emulation(a, emu)
+    assert_emulation(b, emu)
     assert O.relerr(a, b) < 5e-3
 
 

@@ -9,6 +9,12 @@
 | decode_partials + merge  | fp64 attention within 1e-2 (reference bound, tests/test_int4_kv.py:190) and 0.5%;           |
 |                          | single-tile = textbook softmax; segment-count invariance; constant V; planted mistakes     |
 | merge_partials           | two-segment closed form (LSE algebra)                                                       |
+| segment_lse, merge_lse   | scipy's logsumexp of the scores (natural log), a pure-Python loop, empty segments -> -inf   |
+| value_probabilities      | planted mistake: the zero-point sum taken on the unrounded P * s_v fails fp64 where the     |
+|                          | value codes equal their zero points on all but two keys                                    |
+| max_row_relerr           | hand-computed rows                                                                          |
+| quantize_int4 (_fma32)   | rows where FMA and mul-then-add round differently: the oracle takes the FMA code (assumed,  |
+|                          | parity unpinned against the reference's Triton store)                                       |
 | quantize_int4/int8/store | reference error bounds (tests/test_k8v4_kv.py:147-156), hand-built rows, slot -1 skipped    |
 | round_half_away          | known answers incl. fp32 `x + 0.5` rounding                                                 |
 | rht                      | R R^T = hs I, Sylvester entries (-1)^popcount(i & j), pure-Python hash of the signs          |
@@ -421,3 +427,120 @@ def test_dequant_then_attend_matches_fp64():
     ref = O.attention_f64(q, K, V, n, 0.2)
     got = O.prefill_dequant_attend(q, v, row, n, 0.2, segment=1024)
     assert O.relerr(got, ref) < 1e-2
+
+
+# ----------------------------------------------------------------------------------------- log-sum-exp statistics
+
+def _lse_loop(scores):
+    import math
+    mx = max(scores)
+    return mx + math.log(sum(math.exp(x - mx) for x in scores))
+
+
+def test_segment_and_merged_lse_closed_form():
+    """(m, l) of a segment in log2 units, as the kernels keep them, give the natural-log LSE of its scores."""
+    from scipy.special import logsumexp
+    rng = np.random.default_rng(30)
+    s = rng.standard_normal(37) * 4.0                          # natural-log scores of one row
+    bounds = [(0, 10), (10, 10), (10, 37)]                       # the middle segment is empty
+    ms, ls = [], []
+    for lo, hi in bounds:
+        if lo == hi:
+            ms.append(-np.inf)
+            ls.append(0.0)
+            continue
+        m = (s[lo:hi] * O.LOG2E).max()
+        ms.append(m)
+        ls.append(np.exp2(s[lo:hi] * O.LOG2E - m).sum())
+    ms, ls = np.array(ms, np.float32), np.array(ls, np.float32)
+    seg = O.segment_lse(ms, ls)
+    for k, (lo, hi) in enumerate(bounds):
+        if lo == hi:
+            assert seg[k] == -np.inf
+        else:
+            assert abs(seg[k] - logsumexp(s[lo:hi])) < 2e-5
+            assert abs(seg[k] - _lse_loop(list(s[lo:hi]))) < 2e-5
+    assert abs(O.merge_lse(ms[None], ls[None])[0] - logsumexp(s)) < 2e-5
+    assert O.merge_lse(np.full((1, 3), -np.inf, np.float32), np.zeros((1, 3), np.float32))[0] == -np.inf
+
+
+def test_emulated_partials_give_the_fp64_lse():
+    """The emulation's per-segment (m, l), folded, equal the fp64 logsumexp of scale * q . k over the visible keys."""
+    from scipy.special import logsumexp
+    rng = np.random.default_rng(31)
+    n, nq, nkv, hs, T = 500, 4, 2, 32, 2
+    for fmt in ("int4", "int8"):
+        v, row = _tiny_cache(rng, n, nkv, hs, 16, fmt)
+        q = O.round_bf16(rng.standard_normal((T, nq, hs)).astype(np.float32))
+        _, m, l = O.decode_partials(q, v, row, n, 0.3, 5, tile=32)
+        K, _ = O.dequant_f64(v, row, n)
+        got = O.merge_lse(m, l)
+        for t in range(T):
+            for h in range(nq):
+                vis = n - T + t + 1
+                want = logsumexp(0.3 * (K[:vis, h // (nq // nkv)] @ q[t, h].astype(np.float64)))
+                assert abs(got[t, h] - want) < 1e-4, (fmt, t, h)
+
+
+def _dead_values(rng, v, row, n, live):
+    """Value codes equal to their zero point (value 0) on every key but `live` random ones."""
+    zp = (v.value_word & np.uint32(0xF)).astype(np.uint8)
+    v.value[...] = zp[..., None] | (zp[..., None] << 4)
+    for pos in rng.choice(n, live, replace=False):
+        v.value[row[pos // 16], pos % 16] = rng.integers(0, 256, v.value.shape[-1:], dtype=np.uint8)
+
+
+def test_planted_unrounded_zero_point_sum_fails_the_fp64_check(monkeypatch):
+    """int4_kv.py:90-94: the zero-point correction must use the same bf16-rounded P * s_v as the PV product. With
+    all but two keys' values at their zero points the true output is small, and the rounding gap of the unrounded
+    variant (about 2^-9 of P s_v zp per key, over every key) dominates it."""
+    for seed in (21, 22, 23):
+        rng = np.random.default_rng(seed)
+        n = 600
+        v, row = _tiny_cache(rng, n, 2, 32, 16)
+        _dead_values(rng, v, row, n, 2)
+        q = O.round_bf16(rng.standard_normal((2, 4, 32)).astype(np.float32))
+        K, V = O.dequant_f64(v, row, n)
+        ref = O.attention_f64(q, K, V, n, 0.2)
+        assert O.relerr(O.decode_emulated(q, v, row, n, 0.2, 2), ref) < 5e-3
+        with monkeypatch.context() as mp:
+            mp.setattr(O, "value_probabilities", lambda P, s, z: (O.round_bf16(P * s[None, :]),
+                                                                  ((P * s[None, :]) * z[None, :]).sum(
+                                                                      axis=1, dtype=np.float32)))
+            assert O.relerr(O.decode_emulated(q, v, row, n, 0.2, 2), ref) > 3e-2
+
+
+def test_max_row_relerr_hand_rows():
+    ref = np.array([[[3.0, 4.0], [1.0, 0.0]]])            # two rows of head size 2, norms 5 and 1
+    o = ref.copy()
+    o[0, 0, 0] += 0.05                                     # row 0: 0.05 / 5 = 1 %
+    o[0, 1, 1] += 0.03                                     # row 1: 0.03 / 1 = 3 %
+    assert abs(O.max_row_relerr(o, ref) - 0.03) < 1e-12
+    assert O.relerr(o, ref) < 0.03                         # the Frobenius figure hides row 1
+
+
+# The oracle's int4 store assumes v * inv + zp is one fused multiply-add (k8v4_ops.py:55-56). These rows (min, max,
+# probe), all bf16 values, put the probe within an ulp of a rounding boundary, where a mul-then-add store would pick the
+# other code.
+FMA_ROWS = [(-2.5625, 2.28125, -1.453125, 3, 4), (-2.671875, 2.171875, -1.453125, 3, 4),
+            (-0.61328125, 0.30859375, -0.4609375, 2, 3), (-2.515625, 2.171875, -2.34375, 0, 1)]   # bf16-exact
+
+
+def fma_rows(hs):
+    """[len(FMA_ROWS), hs] fp32 rows: min, max, the probe, then zeros; and the probe's FMA code per row."""
+    x = np.zeros((len(FMA_ROWS), hs), np.float32)
+    for i, (lo, hi, probe, _, _) in enumerate(FMA_ROWS):
+        x[i, :3] = (lo, hi, probe)
+    return x, np.array([r[3] for r in FMA_ROWS])
+
+
+def test_store_takes_the_fused_multiply_add_code():
+    x, want = fma_rows(16)
+    codes, _ = O.quantize_int4(x)
+    got = codes[:, 1] & 0xF                                 # channel 2 = low nibble of byte 1
+    assert (got == want).all()
+    for lo, hi, probe, fma_code, muladd_code in FMA_ROWS:   # the two roundings do differ on these probes
+        scale = np.maximum((np.float32(hi) - np.float32(lo)) / np.float32(15.0), np.float32(1e-6))
+        zp = np.clip(O.round_half_away(-np.float32(lo) / scale), 0, 15).astype(np.float32)
+        inv = np.float32(1.0) / scale
+        assert O.round_half_away(np.float32(probe) * inv + zp) == muladd_code != fma_code

@@ -112,8 +112,17 @@ int device_cus();
 // Prefill through the split-KV decode kernel over query slices of at most 4 tokens (causal within each sequence),
 // then the log-sum-exp merge: the path for shapes the MFMA prefill kernel does not take (head 512, more than 12
 // query heads per KV head). Arguments and workspace are those of qp_prefill; defined with the decode kernels.
+// Sequences with skip_seq[i] >= 0 (when given) are left alone.
 int64_t slice_prefill_workspace(const qp_paged_cache *cache, const qp_prefill_args *a);
-int slice_prefill(const qp_paged_cache *cache, const qp_prefill_args *a, hipStream_t stream);
+int slice_prefill(const qp_paged_cache *cache, const qp_prefill_args *a, const int32_t *skip_seq, hipStream_t stream);
+
+// Routed split-KV decode and merge (qp_decode.hip) and prefill (qp_prefill.hip) for qp_attention: a route table
+// gives each short sequence its first segment-buffer row (route_row[i] >= 0) and sends the others to the prefill.
+int decode_routed(const qp_paged_cache *cache, const qp_decode_args *a, const int32_t *route_row, int max_rows,
+                  hipStream_t s);
+int merge_routed(const qp_merge_args *a, const int32_t *row_tok, const int32_t *row_seq, int64_t rows,
+                 const int32_t *skip_seq, hipStream_t s);
+int prefill_run(const qp_paged_cache *cache, const qp_prefill_args *a, const int32_t *skip_seq, hipStream_t s);
 
 // Exact magic division for 0 <= x < 2^31 by d >= 2: m = ceil(2^(31+l) / d), l = ceil(log2 d);
 // x / d == umulhi(x, m) >> (l - 1).
@@ -183,6 +192,61 @@ __device__ __forceinline__ void fwht_wave(float (&x)[E], int lane) {
     }
 }
 
+// Forward randomized Hadamard rotation of a query row held by the four lanes l, l ^ 16, l ^ 32, l ^ 48 of a wave
+// (the lane group g = lane >> 4 holds channels g E .. g E + E - 1 in x): x <- (x D) H with D the +/-1 diagonal
+// (signs, indexed by channel) and H the Sylvester matrix of 4E channels. The butterflies run over channel bits in
+// ascending order, local bits first and then the two lane-group bits, exactly as rht_kernel does for the same row, so
+// the fp32 results are bit-identical to a separate rotation pass.
+template <int E>
+__device__ __forceinline__ void rotate_row_quad(float (&x)[E], const float *signs, int g) {
+#pragma unroll
+  for (int i = 0; i < E; ++i) x[i] *= signs[g * E + i];
+#pragma unroll
+  for (int span = 1; span < E; span <<= 1)
+#pragma unroll
+    for (int i = 0; i < E; ++i)
+      if (!(i & span)) {
+        const float u = x[i], v = x[i + span];
+        x[i] = u + v;
+        x[i + span] = u - v;
+      }
+#pragma unroll
+  for (int ls = 16; ls < 64; ls <<= 1)
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const float v = __shfl_xor(x[i], ls, 64);
+      x[i] = ((g << 4) & ls) ? v - x[i] : x[i] + v;
+    }
+}
+
+// One query row as bf16 (E channels per lane group, 16-byte aligned rows), rotated first when signs is set. The
+// result (bf16 bits, two channels per dword) is what an unrotated caller would have stored after rounding the rotated
+// row to bf16, as the reference feeds its kernel `single_rht(q).to(q.dtype)` (int4_kv.py:326).
+template <int E>
+__device__ __forceinline__ void load_query_row(uint32_t (&out)[E / 2], const uint16_t *row, bool valid,
+                                               const float *signs, int g) {
+  const uint16_t *src = row + E * g;
+#pragma unroll
+  for (int i = 0; i < E / 8; ++i) {
+    const u32x4_t v = valid ? *reinterpret_cast<const u32x4_t *>(src + 8 * i) : u32x4_t{0u, 0u, 0u, 0u};
+    out[4 * i + 0] = v[0];
+    out[4 * i + 1] = v[1];
+    out[4 * i + 2] = v[2];
+    out[4 * i + 3] = v[3];
+  }
+  if (signs) {
+    float x[E];
+#pragma unroll
+    for (int i = 0; i < E / 2; ++i) {
+      x[2 * i] = bf16_lo(out[i]);
+      x[2 * i + 1] = bf16_hi(out[i]);
+    }
+    rotate_row_quad<E>(x, signs, g);
+#pragma unroll
+    for (int i = 0; i < E / 2; ++i) out[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+  }
+}
+
 }  // namespace qp
 
 // ------------------------------------------------------------------------------ shared kernel helpers
@@ -207,12 +271,11 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Per-key scalars of one key from its two words: (a_k, b_k) = (s_k * scale_log2, (128 + zp_k) * a_k) for the key
-// half, (s_v, 128 + zp_v) for the value half; zeros for keys at or past kend.
+// Per-key scalars of one key from its key word: (a_k, b_k) = (s_k * scale_log2, (128 + zp_k) * a_k) (int4 keys,
+// whose operands are 128 + n) or (s_k * scale_log2, 0) (int8 keys); zeros for keys at or past kend.
 template <int KFMT>
-__device__ __forceinline__ float2 key_floats(uint32_t word, bool is_value, bool ok, float scale_log2) {
+__device__ __forceinline__ float2 key_floats(uint32_t word, bool ok, float scale_log2) {
   if (!ok) return make_float2(0.f, 0.f);
-  if (is_value) return make_float2(__uint_as_float(word & 0xFFFFFFF0u), (float)(128u + (word & 0xFu)));
   if constexpr (KFMT == QP_CODES_INT4) {
     const float a = __uint_as_float(word & 0xFFFFFFF0u) * scale_log2;
     return make_float2(a, a * (float)(128u + (word & 0xFu)));
@@ -221,13 +284,14 @@ __device__ __forceinline__ float2 key_floats(uint32_t word, bool is_value, bool 
   }
 }
 
-// The value-half scalars in the decode layout: (s_v, zero-point pair) where the pair holds 128 + zp of this key and
-// of the next one as two bf16 integers (0x4300 | zp each), for a bf16 dot with two rounded P * s_v. Lane i takes the
-// next key's word from lane i + 1 of its 16-lane row (DPP row shift), so the pair is only meaningful for even keys
-// with the next key in the same row; s_v is 0 for keys at or past kend.
+// The value-half scalars in the decode layout: (s_v, zero-point pair) where the pair holds 16 + zp of this key and
+// of the next one as two bf16 integers (0x4180 | zp << 3 each, the offset of the nib_pair16 value operands), for a
+// bf16 dot with two rounded P * s_v. Lane i takes the next key's word from lane i + 1 of its 16-lane row (DPP row
+// shift), so the pair is only meaningful for even keys with the next key in the same row; s_v is 0 for keys at or
+// past kend.
 __device__ __forceinline__ float2 value_floats_paired(uint32_t word, bool ok) {
   const uint32_t next = (uint32_t)__builtin_amdgcn_mov_dpp((int)word, 0x101, 0xF, 0xF, false);  // row_shl:1
-  const uint32_t pair = 0x43004300u | (word & 0xFu) | ((next & 0xFu) << 16);
+  const uint32_t pair = 0x41804180u | ((word & 0xFu) << 3) | ((next & 0xFu) << 19);
   return make_float2(ok ? __uint_as_float(word & 0xFFFFFFF0u) : 0.f, __uint_as_float(pair));
 }
 

@@ -19,13 +19,16 @@
 //     AGPRs through inline-assembly MFMAs, the query operands read from LDS) and for head 512, where more than 16
 //     rows run as workgroups of whole tokens.
 //   * QK^T runs as S^T = K Q^T on v_mfma_f32_16x16x32_bf16 with the K tile as the A operand: nibbles become exact
-//     bf16 integers 128 + n (one v_bitop3 per pair plus shifts), the Q operand is permuted to match. The S^T
+//     bf16 integers 128 + n (one v_bitop3 per pair plus shifts), the Q operand is permuted to match; a caller that
+//     passes the rotation signs gets its unrotated query rows rotated in registers as they load. The S^T
 //     accumulator layout (4 keys x 1 query row per lane) is exactly the B operand layout of O^T = V^T P^T, so P
 //     never leaves registers.
 //   * V is read from LDS as 16-bit pieces of two keys, giving per lane the per-channel key pairs the V^T A operand
 //     needs.
-//   * The +128 offsets are removed through per-key scalars: S uses (128 + zp_k) * sum(q); the output subtracts
-//     sum(P_v16 * (128 + zp_v)), accumulated from the same rounded P_v16 that feeds the MFMA.
+//   * V codes become 16 + n (nib_pair16), keys 128 + n. The offsets are removed through per-key scalars: S uses
+//     (128 + zp_k) * sum(q); the output subtracts sum(P_v16 * (16 + zp_v)), accumulated from the same rounded P_v16
+//     that feeds the MFMA. The small value offset keeps the fp32 cancellation of acc - sum P_v16 (16 + zp_v) small
+//     even where most values sit at their zero point.
 //   * Online softmax in base 2 with a lazy rescale (only when a row maximum grows by more than 2^8); the waves'
 //     states merge in LDS at the end (each wave parking its rows in its own stage buffers where they fit) and the
 //     workgroup writes one (acc, m, l) partial per row.
@@ -62,14 +65,21 @@ struct DecodeParams {
   // Token groups (no slices): when tok_group > 0, workgroup z takes tokens [g * tok_group, (g + 1) * tok_group) of
   // sequence z / tok_groups, g = z % tok_groups, so that the query rows of a workgroup fit fewer row tiles.
   int32_t tok_group, tok_groups;
+  // Routed batches (token groups): route_row[i] is the first segment-buffer row of sequence i's query tokens, or -1
+  // when another kernel serves the sequence (its workgroups then stop at once). Without it, the rows are the
+  // tokens' own indices.
+  const int32_t *route_row;
+  // Forward rotation of the query rows as they load (signs of the randomized Hadamard diagonal), or null when q is
+  // already in the cache's domain.
+  const float *qsigns;
 };
 
-// The work of one workgroup: query tokens [q0, q0 + T) of sequence seq, context n for its last token, keys
-// [kstart, kend) of segment seg_idx. Segments follow the sequence's full context (as the merge does), so in slice mode
-// a segment can lie wholly past the slice's context: its statistics are written as empty (m = -inf, l = 0) for the
-// merge and the workgroup stops.
+// The work of one workgroup: query tokens [q0, q0 + T) of sequence seq, whose segment-buffer rows start at row0,
+// context n for its last token, keys [kstart, kend) of segment seg_idx. Segments follow the sequence's full context
+// (as the merge does), so with slices or token groups a segment can lie wholly past the work's context: its
+// statistics are written as empty (m = -inf, l = 0) for the merge and the workgroup stops.
 struct DecodeWork {
-  int seq, q0, T, n, kstart, kend;
+  int seq, q0, row0, T, n, kstart, kend;
 };
 
 __device__ __forceinline__ bool decode_work(const DecodeParams &p, int G, int h, int seg_idx, DecodeWork &d) {
@@ -78,6 +88,7 @@ __device__ __forceinline__ bool decode_work(const DecodeParams &p, int G, int h,
     const int4 sl = p.slices[blockIdx.z];
     d.seq = sl.x;
     d.q0 = sl.y;
+    d.row0 = d.q0;
     d.T = sl.z;
     d.n = sl.w;
     if (d.T <= 0) return false;
@@ -86,13 +97,20 @@ __device__ __forceinline__ bool decode_work(const DecodeParams &p, int G, int h,
     d.seq = blockIdx.z / p.tok_groups;
     const int t0 = (blockIdx.z - d.seq * p.tok_groups) * p.tok_group;
     const int qa = p.cu_q[d.seq], tf = p.cu_q[d.seq + 1] - qa;
+    int rbase = qa;
+    if (p.route_row) {
+      rbase = p.route_row[d.seq];
+      if (rbase < 0) return false;
+    }
     d.q0 = qa + t0;
+    d.row0 = rbase + t0;
     d.T = min(p.tok_group, tf - t0);
     nfull = p.used_k[d.seq];
     d.n = nfull - tf + t0 + d.T;  // context of the group's last token
   } else {
     d.seq = blockIdx.z;
     d.q0 = p.cu_q[d.seq];
+    d.row0 = d.q0;
     d.T = p.cu_q[d.seq + 1] - d.q0;
     d.n = p.used_k[d.seq];
     nfull = d.n;
@@ -104,7 +122,7 @@ __device__ __forceinline__ bool decode_work(const DecodeParams &p, int G, int h,
   if (d.kstart < d.kend) return true;
   if ((p.slices || p.tok_group > 0) && d.kstart < nfull) {
     for (int r = threadIdx.x; r < d.T * G; r += blockDim.x) {
-      const int64_t o = (int64_t)(d.q0 + r / G) * p.sts0 + (int64_t)(h * G + r % G) * p.sts1 + seg_idx;
+      const int64_t o = (int64_t)(d.row0 + r / G) * p.sts0 + (int64_t)(h * G + r % G) * p.sts1 + seg_idx;
       p.smax[o] = -INFINITY;
       p.ssum[o] = 0.f;
     }
@@ -127,7 +145,7 @@ struct WaveState {
   bf16x8_t qop[NCT][kNmi];              // B operand of S^T = K Q^T
   float qsum[NCT];                      // sum of the row's query channels (int4 zero-point term)
   int row_pos[NCT];                     // absolute position of the row's query token
-  float m[NCT], l[NCT], c[NCT];         // running max (log2 units), sum of P, sum of P_v16 (128 + zp_v)
+  float m[NCT], l[NCT], c[NCT];         // running max (log2 units), sum of P, sum of P_v16 (16 + zp_v)
   f32x4_t acc[NCT][kNb * 4];            // O^T tiles: tile (b, c) row j -> channel 64 b + 16 g + 4 j + c
 };
 
@@ -141,11 +159,13 @@ __device__ __forceinline__ void init_state(WaveState<HS, KFMT, NCT> &st, const D
     const bool rv = r < R;
     const int t = (rv ? r : R - 1) / G, j = (rv ? r : R - 1) % G;
     st.row_pos[ct] = n - T + t;
-    const uint16_t *qr = p.q + (int64_t)(q0 + t) * p.qs0 + (int64_t)(h * G + j) * p.qs1 + (HS / 4) * g;
+    const uint16_t *qr = p.q + (int64_t)(q0 + t) * p.qs0 + (int64_t)(h * G + j) * p.qs1;
+    uint32_t qw[HS / 8];  // channels (HS / 4) g .. + HS / 4 of the row, two per dword (rotated when asked)
+    load_query_row<HS / 4>(qw, qr, rv, p.qsigns, g);
     float qs = 0.f;
 #pragma unroll
     for (int mi = 0; mi < HS / 32; ++mi) {
-      const u32x4_t x = rv ? *reinterpret_cast<const u32x4_t *>(qr + 8 * mi) : u32x4_t{0u, 0u, 0u, 0u};
+      const u32x4_t x = u32x4_t{qw[4 * mi], qw[4 * mi + 1], qw[4 * mi + 2], qw[4 * mi + 3]};
       if constexpr (KFMT == QP_CODES_INT4) {
         // K operand element order per 8 channels: (c0, c4, c1, c5, c2, c6, c3, c7), see nib_pair.
         qs += bf16_lo(x[0]) + bf16_hi(x[0]) + bf16_lo(x[1]) + bf16_hi(x[1]) + bf16_lo(x[2]) + bf16_hi(x[2]) +
@@ -367,7 +387,7 @@ __device__ __forceinline__ void chunk_finish(WaveState<HS, KFMT, NCT> &st, const
       const float p1 = __builtin_amdgcn_exp2f(s[sub][j0 + 1] - mu);
       lsum += p0 + p1;
       const uint32_t pk = pack_bf16x2(p0 * kf[sub][j0].z, p1 * kf[sub][j0 + 1].z);
-      // sum of P16 (128 + zp_v) over the key pair, from the same rounded P16 the MFMA takes
+      // sum of P16 (16 + zp_v) over the key pair, from the same rounded P16 the MFMA takes
       csum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk),
                                              __builtin_bit_cast(bf16x2_t, __float_as_uint(kf[sub][j0].w)), csum,
                                              false);
@@ -384,7 +404,7 @@ __device__ __forceinline__ void chunk_finish(WaveState<HS, KFMT, NCT> &st, const
     for (int c = 0; c < 4; ++c) {
       u32x4_t vv;
 #pragma unroll
-      for (int d = 0; d < 4; ++d) vv[d] = nib_pair(cr.vx[b][d] >> (4 * c));
+      for (int d = 0; d < 4; ++d) vv[d] = nib_pair16(cr.vx[b][d], c);
       const bf16x8_t vop = as_bf16x8(vv);
       if constexpr (acc_in_agprs<HS, KFMT, NCT>()) {
         pv_tile_agpr<NCT>(st.acc, b * 4 + c, vop, pop, b == kNb - 1 && c == 3);
@@ -415,7 +435,7 @@ __device__ __forceinline__ void compute_chunk(WaveState<HS, KFMT, NCT> &st, cons
 // launch. smem must hold merge_lds_bytes and be free (every wave done with its stages once the first barrier passes).
 template <int HS, int KFMT, int NCT, int WAVES>
 __device__ __forceinline__ void finish_workgroup(WaveState<HS, KFMT, NCT> &st, uint8_t *smem, const DecodeParams &p,
-                                                 int w, int col, int g, int q0, int T, int G, int h, int seg_idx) {
+                                                 int w, int col, int g, int row0, int T, int G, int h, int seg_idx) {
   constexpr int kORow = HS + 4;           // floats per parked row (padding spreads the rows over the banks)
   constexpr int kRows = NCT * 16;         // rows per wave slice
   const int R = T * G;
@@ -470,7 +490,7 @@ __device__ __forceinline__ void finish_workgroup(WaveState<HS, KFMT, NCT> &st, u
       sum.w += v.w;
     }
     const int t = r / G, j = r % G;
-    float *dst = p.so + (int64_t)(q0 + t) * p.sos0 + (int64_t)(h * G + j) * p.sos1 + (int64_t)seg_idx * p.sos2;
+    float *dst = p.so + (int64_t)(row0 + t) * p.sos0 + (int64_t)(h * G + j) * p.sos1 + (int64_t)seg_idx * p.sos2;
     reinterpret_cast<float4 *>(dst)[c4] = sum;
   }
   if (w == 0 && g == 0) {
@@ -487,7 +507,7 @@ __device__ __forceinline__ void finish_workgroup(WaveState<HS, KFMT, NCT> &st, u
           if (mw != -INFINITY) L += st_l[ww * kRows + r] * __builtin_amdgcn_exp2f(mw - M);
         }
         const int t = r / G, j = r % G;
-        const int64_t o = (int64_t)(q0 + t) * p.sts0 + (int64_t)(h * G + j) * p.sts1 + seg_idx;
+        const int64_t o = (int64_t)(row0 + t) * p.sts0 + (int64_t)(h * G + j) * p.sts1 + seg_idx;
         p.smax[o] = M;
         p.ssum[o] = L;
       }
@@ -502,7 +522,7 @@ __device__ __forceinline__ void finish_workgroup(WaveState<HS, KFMT, NCT> &st, u
 template <int HS, int KFMT, int NCT, int WAVES, int REGION>
 __device__ __forceinline__ void finish_workgroup_own(WaveState<HS, KFMT, NCT> &st, uint8_t *smem, float *st_m,
                                                      float *st_l, const DecodeParams &p, int w, int col, int g,
-                                                     int q0, int T, int G, int h, int seg_idx) {
+                                                     int row0, int T, int G, int h, int seg_idx) {
   constexpr int kORow = HS + 4;
   constexpr int kRows = NCT * 16;
   static_assert(kRows * kORow * 4 <= REGION, "a wave's stage buffers hold its parked rows");
@@ -557,7 +577,7 @@ __device__ __forceinline__ void finish_workgroup_own(WaveState<HS, KFMT, NCT> &s
       sum.w = fmaf(v.w, f, sum.w);
     }
     const int t = r / G, j = r % G;
-    float *dst = p.so + (int64_t)(q0 + t) * p.sos0 + (int64_t)(h * G + j) * p.sos1 + (int64_t)seg_idx * p.sos2;
+    float *dst = p.so + (int64_t)(row0 + t) * p.sos0 + (int64_t)(h * G + j) * p.sos1 + (int64_t)seg_idx * p.sos2;
     reinterpret_cast<float4 *>(dst)[c4] = sum;
   }
   if (w == 0 && g == 0) {
@@ -574,7 +594,7 @@ __device__ __forceinline__ void finish_workgroup_own(WaveState<HS, KFMT, NCT> &s
           if (mw != -INFINITY) L += st_l[ww * kRows + r] * __builtin_amdgcn_exp2f(mw - M);
         }
         const int t = r / G, j = r % G;
-        const int64_t o = (int64_t)(q0 + t) * p.sts0 + (int64_t)(h * G + j) * p.sts1 + seg_idx;
+        const int64_t o = (int64_t)(row0 + t) * p.sts0 + (int64_t)(h * G + j) * p.sts1 + seg_idx;
         p.smax[o] = M;
         p.ssum[o] = L;
       }
@@ -591,7 +611,7 @@ constexpr int merge_lds_bytes() {
 // several workgroups per CU.
 template <int HS, int KFMT, int NCT, int WAVES>
 __device__ __forceinline__ void finish_workgroup_serial(WaveState<HS, KFMT, NCT> &st, uint8_t *smem, const DecodeParams &p,
-                                                 int w, int col, int g, int q0, int T, int G, int h, int seg_idx) {
+                                                 int w, int col, int g, int row0, int T, int G, int h, int seg_idx) {
   constexpr int kORow = HS + 4;
   const int R = T * G;
 #pragma unroll
@@ -649,7 +669,7 @@ __device__ __forceinline__ void finish_workgroup_serial(WaveState<HS, KFMT, NCT>
   for (int idx = threadIdx.x; idx < R * (HS / 4); idx += WAVES * 64) {
     const int r = idx / (HS / 4), c4 = idx % (HS / 4);
     const int t = r / G, j = r % G;
-    float *dst = p.so + (int64_t)(q0 + t) * p.sos0 + (int64_t)(h * G + j) * p.sos1 + (int64_t)seg_idx * p.sos2;
+    float *dst = p.so + (int64_t)(row0 + t) * p.sos0 + (int64_t)(h * G + j) * p.sos1 + (int64_t)seg_idx * p.sos2;
     reinterpret_cast<float4 *>(dst)[c4] = reinterpret_cast<const float4 *>(obuf + r * kORow)[c4];
   }
   if (w == 0 && g == 0) {
@@ -666,7 +686,7 @@ __device__ __forceinline__ void finish_workgroup_serial(WaveState<HS, KFMT, NCT>
           if (mw != -INFINITY) L += st_l[(ww * NCT + ct) * 16 + col] * __builtin_amdgcn_exp2f(mw - M);
         }
         const int t = r / G, j = r % G;
-        const int64_t o = (int64_t)(q0 + t) * p.sts0 + (int64_t)(h * G + j) * p.sts1 + seg_idx;
+        const int64_t o = (int64_t)(row0 + t) * p.sts0 + (int64_t)(h * G + j) * p.sts1 + seg_idx;
         p.smax[o] = M;
         p.ssum[o] = L;
       }
@@ -766,7 +786,7 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(const DecodeParams p) 
   const int G = p.num_q_heads / p.num_kv_heads;
   DecodeWork d;
   if (!decode_work(p, G, h, seg_idx, d)) return;
-  const int seq = d.seq, q0 = d.q0, T = d.T, n = d.n, kstart = d.kstart, kend = d.kend;
+  const int seq = d.seq, q0 = d.q0, row0 = d.row0, T = d.T, n = d.n, kstart = d.kstart, kend = d.kend;
   const int col = lane & 15, g = lane >> 4;
 
   WaveState<HS, KFMT, NCT> st;
@@ -796,7 +816,7 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(const DecodeParams p) 
     {
       const int kk = lane & 31;
       const float2 f = lane >= 32 ? value_floats_paired(regs.w, k0 + kk < kend)
-                                  : key_floats<KFMT>(regs.w, false, k0 + kk < kend, p.scale_log2);
+                                  : key_floats<KFMT>(regs.w, k0 + kk < kend, p.scale_log2);
       *reinterpret_cast<float2 *>(wl + Sh::kFOff + kk * 16 + (lane < 32 ? 0 : 8)) = f;
     }
     wave_sync();
@@ -805,7 +825,7 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(const DecodeParams p) 
     compute_chunk<HS, KFMT, NCT, Sh::kKRow, Sh::kVRow>(st, wl, wl + Sh::kVOff, wl + Sh::kFOff, k0, kend, causal_lim,
                                                        col, g, &rsc[w][lane]);
   }
-  finish_workgroup_serial<HS, KFMT, NCT, kWaves>(st, smem, p, w, col, g, q0, T, G, h, seg_idx);
+  finish_workgroup_serial<HS, KFMT, NCT, kWaves>(st, smem, p, w, col, g, row0, T, G, h, seg_idx);
 }
 
 // ------------------------------------------------------- HND page spans: HBM -> LDS direct, double-buffered
@@ -879,7 +899,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
   const int G = p.num_q_heads / p.num_kv_heads;
   DecodeWork d;
   if (!decode_work(p, G, h, seg_idx, d)) return;
-  const int seq = d.seq, q0 = d.q0, T = d.T, n = d.n, kstart = d.kstart, kend = d.kend;
+  const int seq = d.seq, q0 = d.q0, row0 = d.row0, T = d.T, n = d.n, kstart = d.kstart, kend = d.kend;
   const int col = lane & 15, g = lane >> 4;
 
   // Chunks are handed out in key order: the first kStages of every wave statically (chunk w + s * WAVES), the rest
@@ -926,7 +946,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
       const bool is_v = lane >= 32;
       const uint32_t word = *reinterpret_cast<const uint32_t *>(stage + kk * Sh::kCell + (is_v ? kWordV : kWordK));
       const float2 f = is_v ? value_floats_paired(word, k0 + kk < kend)
-                            : key_floats<KFMT>(word, false, k0 + kk < kend, p.scale_log2);
+                            : key_floats<KFMT>(word, k0 + kk < kend, p.scale_log2);
       *reinterpret_cast<float2 *>(reinterpret_cast<uint8_t *>(fl) + kk * 16 + (is_v ? 8 : 0)) = f;
     }
     wave_sync();
@@ -956,10 +976,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
     }
   }
   if constexpr (kOwnMerge)
-    finish_workgroup_own<HS, KFMT, NCT, WAVES, kStages * 2 * Sh::kHalf>(st, smem, mst[0], mst[1], p, w, col, g, q0, T,
+    finish_workgroup_own<HS, KFMT, NCT, WAVES, kStages * 2 * Sh::kHalf>(st, smem, mst[0], mst[1], p, w, col, g, row0, T,
                                                                         G, h, seg_idx);
-  else if constexpr (kParMerge) finish_workgroup<HS, KFMT, NCT, WAVES>(st, smem, p, w, col, g, q0, T, G, h, seg_idx);
-  else finish_workgroup_serial<HS, KFMT, NCT, WAVES>(st, smem, p, w, col, g, q0, T, G, h, seg_idx);
+  else if constexpr (kParMerge) finish_workgroup<HS, KFMT, NCT, WAVES>(st, smem, p, w, col, g, row0, T, G, h, seg_idx);
+  else finish_workgroup_serial<HS, KFMT, NCT, WAVES>(st, smem, p, w, col, g, row0, T, G, h, seg_idx);
 }
 
 // ------------------------------------------------------------------------------------------------- merge
@@ -977,6 +997,11 @@ struct MergeParams {
   int64_t ls0, ls1;
   const float *signs;
   float out_scale;
+  // Routed rows: workgroup x merges segment-buffer row x for token row_tok[x] of sequence row_seq[x] (-1: unused
+  // row). Without them, row x is token x.
+  const int32_t *row_tok, *row_seq;
+  // Plain rows only: sequences with skip_seq[i] >= 0 are merged elsewhere (null: none).
+  const int32_t *skip_seq;
 };
 
 // One workgroup of 256 threads per (token, query head). Thread t owns channels 4 (t % (HS/4)) .. +3 of the segments
@@ -990,18 +1015,26 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
   __shared__ float pm[256], pl[256];
   __shared__ float row[2][1024];
   __shared__ float stat[2];
-  const int tok = blockIdx.x, head = blockIdx.y, t = threadIdx.x;
-  int lo = 0, hi = p.num_seqs - 1;
-  while (lo < hi) {  // last sequence whose first query token is <= tok
-    const int mid = (lo + hi + 1) >> 1;
-    if (p.cu_q[mid] <= tok) lo = mid;
-    else hi = mid - 1;
+  const int srow = blockIdx.x, head = blockIdx.y, t = threadIdx.x;
+  int tok = srow, lo = 0;
+  if (p.row_tok) {
+    tok = p.row_tok[srow];
+    if (tok < 0) return;
+    lo = p.row_seq[srow];
+  } else {
+    int hi = p.num_seqs - 1;
+    while (lo < hi) {  // last sequence whose first query token is <= tok
+      const int mid = (lo + hi + 1) >> 1;
+      if (p.cu_q[mid] <= tok) lo = mid;
+      else hi = mid - 1;
+    }
+    if (p.skip_seq && p.skip_seq[lo] >= 0) return;
   }
   const int n = p.used_k[lo];
   const int seg = (n + p.num_segments * QP_DECODE_TILE - 1) / (p.num_segments * QP_DECODE_TILE) * QP_DECODE_TILE;
   const int active = seg > 0 ? min(p.num_segments, (n + seg - 1) / seg) : 0;
-  const float *mrow = p.smax + (int64_t)tok * p.sts0 + (int64_t)head * p.sts1;
-  const float *lrow = p.ssum + (int64_t)tok * p.sts0 + (int64_t)head * p.sts1;
+  const float *mrow = p.smax + (int64_t)srow * p.sts0 + (int64_t)head * p.sts1;
+  const float *lrow = p.ssum + (int64_t)srow * p.sts0 + (int64_t)head * p.sts1;
   // without the rotation the channels split over gridDim.z workgroups (more CUs reading the partials); the rotation
   // needs the whole row in one workgroup
   const int width = p.head_size / gridDim.z, c0 = blockIdx.z * width;
@@ -1018,7 +1051,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
   if (sg < groups) {
     // batches of kBatch segments: every load of a batch is issued before any of it is used
     constexpr int kBatch = 16;
-    const float *orow = p.so + (int64_t)tok * p.sos0 + (int64_t)head * p.sos1 + c0 + 4 * cq;
+    const float *orow = p.so + (int64_t)srow * p.sos0 + (int64_t)head * p.sos1 + c0 + 4 * cq;
     // rows are requested for every allocated segment (those past `active` are read but ignored), so the loads do not
     // wait for the context length
     for (int s0 = sg; s0 < p.num_segments; s0 += kBatch * groups) {
@@ -1137,8 +1170,10 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
 
 // Query slices of every sequence for the slice prefill: tokens [t0, t0 + ts) of sequence i (the last one shorter),
 // each with the context of its last token, listed sequence by sequence; unused entries of the table get count 0.
+// Sequences with skip_seq[i] >= 0 (when given) get no slices.
 __global__ __launch_bounds__(256) void build_slices_kernel(const int32_t *cu_q, const int32_t *used_k, int num_seqs,
-                                                           int ts, int max_slices, int4 *slices) {
+                                                           int ts, int max_slices, const int32_t *skip_seq,
+                                                           int4 *slices) {
   __shared__ int off[257];
   int base = 0;
   for (int s0 = 0; s0 < num_seqs; s0 += 256) {
@@ -1148,7 +1183,7 @@ __global__ __launch_bounds__(256) void build_slices_kernel(const int32_t *cu_q, 
       q0 = cu_q[i];
       T = cu_q[i + 1] - q0;
       n = used_k[i];
-      cnt = T > 0 ? (T + ts - 1) / ts : 0;
+      cnt = T > 0 && !(skip_seq && skip_seq[i] >= 0) ? (T + ts - 1) / ts : 0;
     }
     off[threadIdx.x] = cnt;
     __syncthreads();
@@ -1232,7 +1267,10 @@ int dispatch_decode(const DecodeParams &p, int kfmt, int nct, dim3 grid, bool sp
 
 }  // namespace
 
-extern "C" int qp_decode_splitkv(const qp_paged_cache *cache, const qp_decode_args *a, qp_stream_t stream) {
+namespace {
+
+// Argument checks shared by the plain and the routed decode (routed batches skip the query-count checks).
+int check_decode(const qp_paged_cache *cache, const qp_decode_args *a, bool routed) {
   QP_REQUIRE(cache && a, "qp_decode_splitkv: null argument");
   QP_REQUIRE(cache->key.codes && cache->key.words && cache->value.codes && cache->value.words,
              "qp_decode_splitkv: null cache view");
@@ -1248,13 +1286,16 @@ extern "C" int qp_decode_splitkv(const qp_paged_cache *cache, const qp_decode_ar
              "qp_decode_splitkv: query heads must be a multiple of KV heads");
   QP_SUPPORTED(cache->block_size >= 16 && cache->block_size % 16 == 0,
                "qp_decode_splitkv: block size must be a multiple of 16");
-  QP_REQUIRE(a->max_query_len >= 1 && a->max_query_len <= QP_DECODE_MAX_QUERY,
-             "qp_decode_splitkv: 1..4 query tokens per sequence");
   const int G = a->num_q_heads / cache->num_kv_heads;
-  const int rows = a->max_query_len * G;
-  QP_SUPPORTED(rows <= 32, "qp_decode_splitkv: more than 32 query rows per KV head");
+  QP_SUPPORTED(G <= 32, "qp_decode_splitkv: more than 32 query heads per KV head");
+  QP_SUPPORTED(hs != 512 || G <= 16, "qp_decode_splitkv: head 512 takes at most 16 query heads per KV head");
+  if (!routed) {
+    QP_REQUIRE(a->max_query_len >= 1 && a->max_query_len <= QP_DECODE_MAX_QUERY,
+               "qp_decode_splitkv: 1..4 query tokens per sequence");
+    QP_SUPPORTED(a->max_query_len * G <= 32, "qp_decode_splitkv: more than 32 query rows per KV head");
+    QP_REQUIRE(a->num_tokens <= a->segm_rows, "qp_decode_splitkv: more query tokens than segment-buffer rows");
+  }
   QP_REQUIRE(a->num_segments >= 1 && a->num_segments <= 2048, "qp_decode_splitkv: 1..2048 segments");
-  QP_REQUIRE(a->num_tokens <= a->segm_rows, "qp_decode_splitkv: more query tokens than segment-buffer rows");
   QP_REQUIRE(a->num_seqs >= 0 && a->num_seqs <= 65535, "qp_decode_splitkv: bad sequence count");
   for (int i = 0; i < 3; ++i) {
     QP_REQUIRE(cache->key.code_stride[i] % 4 == 0 && cache->value.code_stride[i] % 4 == 0,
@@ -1270,9 +1311,10 @@ extern "C" int qp_decode_splitkv(const qp_paged_cache *cache, const qp_decode_ar
   QP_REQUIRE(aligned(a->segm_output, 16) && a->segm_output_stride[0] % 4 == 0 && a->segm_output_stride[1] % 4 == 0 &&
                  a->segm_output_stride[2] % 4 == 0,
              "qp_decode_splitkv: segment output rows must be 16-byte aligned");
-  if (a->num_seqs == 0 || a->num_tokens == 0) return QP_OK;
+  return QP_OK;
+}
 
-  DecodeParams p;
+void decode_params(const qp_paged_cache *cache, const qp_decode_args *a, DecodeParams &p) {
   cache_params(cache, p);
   p.q = static_cast<const uint16_t *>(a->query);
   p.qs0 = a->query_stride[0];
@@ -1295,31 +1337,11 @@ extern "C" int qp_decode_splitkv(const qp_paged_cache *cache, const qp_decode_ar
   p.slices = nullptr;
   p.tok_group = 0;
   p.tok_groups = 1;
-  int nct = rows > 16 ? 2 : 1;
-  if (nct == 2 && cache->head_size == 512 && G <= 16) {
-    // Two row tiles at head 512 do not fit the registers (the accumulators alone fill the AGPRs); workgroups of
-    // whole tokens with at most 16 rows read the segment once per group instead, which costs far less.
-    p.tok_group = 16 / G;
-    p.tok_groups = (a->max_query_len + p.tok_group - 1) / p.tok_group;
-    nct = 1;
-  }
-  const dim3 grid(a->num_segments, cache->num_kv_heads, a->num_seqs * p.tok_groups);
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  return dispatch_hs(cache, p, nct, grid, s);
+  p.route_row = nullptr;
+  p.qsigns = a->query_signs;
 }
 
-extern "C" int qp_merge_segments(const qp_merge_args *a, qp_stream_t stream) {
-  QP_REQUIRE(a && a->segm_output && a->segm_max && a->segm_expsum && a->cu_seqlens_q && a->seqused_k && a->out,
-             "qp_merge_segments: null argument");
-  QP_REQUIRE(a->head_size >= 4 && a->head_size <= 1024 && a->head_size % 4 == 0 && 256 % (a->head_size / 4) == 0,
-             "qp_merge_segments: head size must be 16, 32, 64, ..., 1024");
-  QP_REQUIRE(!a->rht_signs || (a->head_size & (a->head_size - 1)) == 0,
-             "qp_merge_segments: the fused rotation needs a power-of-two head size");
-  QP_REQUIRE(a->num_segments >= 1 && a->num_segments <= 2048 && a->num_seqs >= 1, "qp_merge_segments: bad sizes");
-  QP_REQUIRE(aligned(a->segm_output, 16) && a->segm_output_stride[2] % 4 == 0 && a->segm_output_stride[1] % 4 == 0 &&
-                 a->segm_output_stride[0] % 4 == 0,
-             "qp_merge_segments: segment output rows must be 16-byte aligned");
-  if (a->num_tokens == 0) return QP_OK;
+MergeParams merge_params(const qp_merge_args *a) {
   MergeParams p;
   p.so = a->segm_output;
   p.sos0 = a->segm_output_stride[0];
@@ -1342,15 +1364,110 @@ extern "C" int qp_merge_segments(const qp_merge_args *a, qp_stream_t stream) {
   p.ls1 = a->lse_stride[1];
   p.signs = a->rht_signs;
   p.out_scale = a->rht_out_scale;
+  p.row_tok = nullptr;
+  p.row_seq = nullptr;
+  p.skip_seq = nullptr;
+  return p;
+}
+
+int check_merge(const qp_merge_args *a) {
+  QP_REQUIRE(a && a->segm_output && a->segm_max && a->segm_expsum && a->cu_seqlens_q && a->seqused_k && a->out,
+             "qp_merge_segments: null argument");
+  QP_REQUIRE(a->head_size >= 4 && a->head_size <= 1024 && a->head_size % 4 == 0 && 256 % (a->head_size / 4) == 0,
+             "qp_merge_segments: head size must be 16, 32, 64, ..., 1024");
+  QP_REQUIRE(!a->rht_signs || (a->head_size & (a->head_size - 1)) == 0,
+             "qp_merge_segments: the fused rotation needs a power-of-two head size");
+  QP_REQUIRE(a->num_segments >= 1 && a->num_segments <= 2048 && a->num_seqs >= 1, "qp_merge_segments: bad sizes");
+  QP_REQUIRE(aligned(a->segm_output, 16) && a->segm_output_stride[2] % 4 == 0 && a->segm_output_stride[1] % 4 == 0 &&
+                 a->segm_output_stride[0] % 4 == 0,
+             "qp_merge_segments: segment output rows must be 16-byte aligned");
+  return QP_OK;
+}
+
+// rows workgroups (one per row: token, or segment-buffer row when routed) per query head.
+int launch_merge(const MergeParams &p, int64_t rows, int num_q_heads, hipStream_t s) {
+  if (rows <= 0) return QP_OK;
   // a few rows need the channel split to spread the partial reads over more CUs; many rows fill the device alone
-  const int64_t rows = (int64_t)a->num_tokens * a->num_q_heads;
-  const int parts = (a->rht_signs || rows >= 1024 || a->head_size < 64) ? 1 : 4;
-  const dim3 grid(a->num_tokens, a->num_q_heads, parts);
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (a->rht_signs) merge_kernel<true><<<grid, 256, 0, s>>>(p);
+  const int parts = (p.signs || rows * num_q_heads >= 1024 || p.head_size < 64) ? 1 : 4;
+  const dim3 grid((unsigned)rows, num_q_heads, parts);
+  if (p.signs) merge_kernel<true><<<grid, 256, 0, s>>>(p);
   else merge_kernel<false><<<grid, 256, 0, s>>>(p);
   return launch_status();
 }
+
+}  // namespace
+
+extern "C" int qp_decode_splitkv(const qp_paged_cache *cache, const qp_decode_args *a, qp_stream_t stream) {
+  const int st = check_decode(cache, a, false);
+  if (st != QP_OK) return st;
+  if (a->num_seqs == 0 || a->num_tokens == 0) return QP_OK;
+  const int G = a->num_q_heads / cache->num_kv_heads;
+  const int rows = a->max_query_len * G;
+  DecodeParams p;
+  decode_params(cache, a, p);
+  int nct = rows > 16 ? 2 : 1;
+  if (nct == 2 && cache->head_size == 512) {
+    // Two row tiles at head 512 do not fit the registers (the accumulators alone fill the AGPRs); workgroups of
+    // whole tokens with at most 16 rows read the segment once per group instead, which costs far less.
+    p.tok_group = 16 / G;
+    p.tok_groups = (a->max_query_len + p.tok_group - 1) / p.tok_group;
+    nct = 1;
+  }
+  const dim3 grid(a->num_segments, cache->num_kv_heads, a->num_seqs * p.tok_groups);
+  return dispatch_hs(cache, p, nct, grid, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int qp_merge_segments(const qp_merge_args *a, qp_stream_t stream) {
+  const int st = check_merge(a);
+  if (st != QP_OK) return st;
+  if (a->num_tokens == 0) return QP_OK;
+  return launch_merge(merge_params(a), a->num_tokens, a->num_q_heads, reinterpret_cast<hipStream_t>(stream));
+}
+
+namespace qp {
+
+// Split-KV decode in token groups: workgroups hold whole tokens, at most max_rows query rows (16: one row tile, 32:
+// two; head 512 always one) when the GQA group has at most 16 heads, one token of two row tiles above that, so the
+// query count of each sequence need not be known on the host. With route_row, sequence i's query tokens take the
+// segment-buffer rows route_row[i] .. + T_i - 1 (route_row[i] < 0: served elsewhere); without it, their own indices.
+int decode_routed(const qp_paged_cache *cache, const qp_decode_args *a, const int32_t *route_row, int max_rows,
+                  hipStream_t s) {
+  const int st = check_decode(cache, a, route_row != nullptr);
+  if (st != QP_OK) return st;
+  if (a->num_seqs == 0 || a->num_tokens == 0) return QP_OK;
+  const int G = a->num_q_heads / cache->num_kv_heads;
+  DecodeParams p;
+  decode_params(cache, a, p);
+  p.route_row = route_row;
+  int nct = 1;
+  if (G <= 16) {
+    int cap = max_rows > 16 && cache->head_size != 512 ? 32 : 16;  // two row tiles or one
+    p.tok_group = cap / G < 1 ? 1 : (cap / G > QP_DECODE_MAX_QUERY ? QP_DECODE_MAX_QUERY : cap / G);
+    nct = p.tok_group * G > 16 ? 2 : 1;
+  } else {
+    p.tok_group = 1;
+    nct = 2;
+  }
+  p.tok_groups = (QP_DECODE_MAX_QUERY + p.tok_group - 1) / p.tok_group;
+  const dim3 grid(a->num_segments, cache->num_kv_heads, a->num_seqs * p.tok_groups);
+  return dispatch_hs(cache, p, nct, grid, s);
+}
+
+// Merge of routed rows: segment-buffer row r (< rows) belongs to token row_tok[r] of sequence row_seq[r]
+// (row_tok[r] < 0: unused). With skip_seq and no row maps, a plain merge over the tokens leaves the sequences with
+// skip_seq[i] >= 0 alone.
+int merge_routed(const qp_merge_args *a, const int32_t *row_tok, const int32_t *row_seq, int64_t rows,
+                 const int32_t *skip_seq, hipStream_t s) {
+  const int st = check_merge(a);
+  if (st != QP_OK) return st;
+  MergeParams p = merge_params(a);
+  p.row_tok = row_tok;
+  p.row_seq = row_seq;
+  p.skip_seq = skip_seq;
+  return launch_merge(p, row_tok ? rows : a->num_tokens, a->num_q_heads, s);
+}
+
+}  // namespace qp
 
 namespace {
 
@@ -1399,10 +1516,11 @@ int64_t slice_prefill_workspace(const qp_paged_cache *cache, const qp_prefill_ar
   return slice_layout(cache, a).total;
 }
 
-int slice_prefill(const qp_paged_cache *cache, const qp_prefill_args *a, hipStream_t s) {
+int slice_prefill(const qp_paged_cache *cache, const qp_prefill_args *a, const int32_t *skip_seq, hipStream_t s) {
   const int hs = cache->head_size;
   const int G = a->num_q_heads / cache->num_kv_heads;
   QP_SUPPORTED(G <= 32, "qp_prefill: at most 32 query heads per KV head");
+  QP_SUPPORTED(hs != 512 || G <= 16, "qp_prefill: head 512 takes at most 16 query heads per KV head");
   if (a->num_seqs == 0 || a->num_tokens == 0) return QP_OK;
   const SliceLayout L = slice_layout(cache, a);
   QP_REQUIRE(a->workspace && a->workspace_bytes >= L.total && aligned(a->workspace, 256),
@@ -1412,7 +1530,8 @@ int slice_prefill(const qp_paged_cache *cache, const qp_prefill_args *a, hipStre
   float *so = reinterpret_cast<float *>(ws + L.off_rows);
   float *sm = reinterpret_cast<float *>(ws + L.off_max);
   float *ss = reinterpret_cast<float *>(ws + L.off_sum);
-  build_slices_kernel<<<1, 256, 0, s>>>(a->cu_seqlens_q, a->seqused_k, a->num_seqs, L.ts, L.max_slices, slices);
+  build_slices_kernel<<<1, 256, 0, s>>>(a->cu_seqlens_q, a->seqused_k, a->num_seqs, L.ts, L.max_slices, skip_seq,
+                                        slices);
   int st = launch_status();
   if (st != QP_OK) return st;
 
@@ -1439,6 +1558,8 @@ int slice_prefill(const qp_paged_cache *cache, const qp_prefill_args *a, hipStre
   p.slices = slices;
   p.tok_group = 0;
   p.tok_groups = 1;
+  p.route_row = nullptr;
+  p.qsigns = a->query_signs;
   const int nct = L.ts * G > 16 ? 2 : 1;
   st = dispatch_hs(cache, p, nct, dim3(L.segments, cache->num_kv_heads, L.max_slices), s);
   if (st != QP_OK) return st;
@@ -1464,7 +1585,7 @@ int slice_prefill(const qp_paged_cache *cache, const qp_prefill_args *a, hipStre
   m.out_stride[1] = a->out_stride[1];
   m.rht_signs = a->rht_signs;
   m.rht_out_scale = a->rht_out_scale;
-  return qp_merge_segments(&m, reinterpret_cast<qp_stream_t>(s));
+  return merge_routed(&m, nullptr, nullptr, 0, skip_seq, s);
 }
 
 }  // namespace qp

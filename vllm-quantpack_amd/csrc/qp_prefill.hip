@@ -55,6 +55,10 @@ struct PrefillParams {
   int32_t num_seqs, num_q_heads, num_kv_heads, block_size, num_splits, bq;
   uint32_t bs_magic, bs_shift;
   float scale_log2;
+  const float *qsigns;     // forward rotation of the query rows as they load (null: q in the cache's domain)
+  const float *osigns;     // inverse rotation of unsplit output rows, out = (o H D) * out_scale (null: none)
+  float out_scale;
+  const int32_t *skip_seq; // sequences with skip_seq[s] >= 0 are served by another kernel (null: none)
 };
 
 constexpr int kPfKeys = 32;  // keys per tile
@@ -534,6 +538,45 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
   }
 }
 
+// Inverse rotation of one output row held in the PV accumulator layout (lane group g holds channel 16 b + 4 g + j at
+// x[4 b + j]): x <- ((x H) D) * scale, with H the Sylvester matrix of HS channels and D the signs. The butterflies
+// run over channel bits in ascending order (j, then g across the lanes l ^ 16 and l ^ 32, then b), as rht_kernel
+// runs them on the same row, so the result equals a separate rotation pass of the fp32 row.
+template <int HS>
+__device__ __forceinline__ void rotate_out_row(float (&x)[HS / 4], const float *signs, float scale, int g) {
+  constexpr int kE = HS / 4;
+#pragma unroll
+  for (int span = 1; span < 4; span <<= 1)
+#pragma unroll
+    for (int i = 0; i < kE; ++i)
+      if (!(i & span)) {
+        const float u = x[i], v = x[i + span];
+        x[i] = u + v;
+        x[i + span] = u - v;
+      }
+#pragma unroll
+  for (int ls = 16; ls < 64; ls <<= 1)
+#pragma unroll
+    for (int i = 0; i < kE; ++i) {
+      const float v = __shfl_xor(x[i], ls, 64);
+      x[i] = ((g << 4) & ls) ? v - x[i] : x[i] + v;
+    }
+#pragma unroll
+  for (int span = 4; span < kE; span <<= 1)
+#pragma unroll
+    for (int i = 0; i < kE; ++i)
+      if (!(i & span)) {
+        const float u = x[i], v = x[i + span];
+        x[i] = u + v;
+        x[i + span] = u - v;
+      }
+#pragma unroll
+  for (int i = 0; i < kE; ++i) {
+    float y = x[i] * signs[16 * (i >> 2) + 4 * g + (i & 3)];
+    x[i] = y * scale;
+  }
+}
+
 template <int HS, int KFMT, int NT, bool SPAN>
 __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillParams p) {
   using Sh = PfShape<HS, KFMT>;
@@ -559,6 +602,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
   const int q0 = p.cu_q[seq], qlen = p.cu_q[seq + 1] - q0;
   const int t0 = (blk - (q0 / BQ + seq)) * BQ;  // first local token of this block
   if (t0 < 0 || t0 >= qlen) return;
+  if (p.skip_seq && p.skip_seq[seq] >= 0) return;
   const int n = p.used_k[seq];
   const int G = p.num_q_heads / p.num_kv_heads;
   const int ntok = min(BQ, qlen - t0);
@@ -580,12 +624,13 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
     const int tok = t0 + 16 * sb + col;
     const bool rv = 16 * sb < BQ && tok < qlen;
     r.row_pos[jt] = rv ? first_pos + 16 * sb + col : -1;
-    const uint16_t *qr =
-        p.q + (int64_t)(q0 + (rv ? tok : 0)) * p.qs0 + (int64_t)(h * G + (rv ? jh : 0)) * p.qs1 + (HS / 4) * g;
+    const uint16_t *qr = p.q + (int64_t)(q0 + (rv ? tok : 0)) * p.qs0 + (int64_t)(h * G + (rv ? jh : 0)) * p.qs1;
+    uint32_t qw[HS / 8];  // channels (HS / 4) g .. + HS / 4 of the row, two per dword (rotated when asked)
+    load_query_row<HS / 4>(qw, qr, rv, p.qsigns, g);
     float qs = 0.f;
 #pragma unroll
     for (int mi = 0; mi < HS / 32; ++mi) {
-      const u32x4_t x = rv ? *reinterpret_cast<const u32x4_t *>(qr + 8 * mi) : u32x4_t{0u, 0u, 0u, 0u};
+      const u32x4_t x = u32x4_t{qw[4 * mi], qw[4 * mi + 1], qw[4 * mi + 2], qw[4 * mi + 3]};
       if constexpr (KFMT == QP_CODES_INT4) {
         qs += bf16_lo(x[0]) + bf16_hi(x[0]) + bf16_lo(x[1]) + bf16_hi(x[1]) + bf16_lo(x[2]) + bf16_hi(x[2]) +
               bf16_lo(x[3]) + bf16_hi(x[3]);
@@ -743,13 +788,31 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
     l += shfl_xor_f(l, 16);
     l += shfl_xor_f(l, 32);
     const float csum = __shfl(r.acc[jt][HS / 16][0], col, 64);
-    if (r.row_pos[jt] < 0) continue;
+    const bool valid = r.row_pos[jt] >= 0;  // the same for the four lanes of a row (lanes col + 16 g)
     const int tt = w + kPfWaves * jt;
     const int64_t tok = q0 + t0 + 16 * (tt / G) + col;
     const int64_t head = h * G + tt % G;
     if (S == 1) {
       const float inv = l > 0.f ? 1.f / l : 0.f;
       uint16_t *orow = p.out + tok * p.os0 + head * p.os1;
+      if (p.osigns) {
+        float x[HS / 4];
+#pragma unroll
+        for (int b = 0; b < HS / 16; ++b) {
+          const f32x4_t a = r.acc[jt][b];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) x[4 * b + j] = (a[j] - csum) * inv;
+        }
+        rotate_out_row<HS>(x, p.osigns, p.out_scale, g);
+        if (valid) {
+#pragma unroll
+          for (int b = 0; b < HS / 16; ++b)
+            *reinterpret_cast<u32x2_t *>(orow + 16 * b + 4 * g) =
+                u32x2_t{pack_bf16x2(x[4 * b], x[4 * b + 1]), pack_bf16x2(x[4 * b + 2], x[4 * b + 3])};
+        }
+        continue;
+      }
+      if (!valid) continue;
 #pragma unroll
       for (int b = 0; b < HS / 16; ++b) {
         const f32x4_t a = r.acc[jt][b];
@@ -758,6 +821,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
         *reinterpret_cast<u32x2_t *>(orow + 16 * b + 4 * g) = u32x2_t{w0, w1};
       }
     } else {
+      if (!valid) continue;
       float *orow = p.so + tok * p.sos0 + head * p.sos1 + (int64_t)split * HS;
 #pragma unroll
       for (int b = 0; b < HS / 16; ++b) {
@@ -837,7 +901,9 @@ extern "C" int64_t qp_prefill_workspace_size(const qp_paged_cache *cache, const 
   return partial_bytes(cache, a, prefill_splits(cache, a, bq));
 }
 
-extern "C" int qp_prefill(const qp_paged_cache *cache, const qp_prefill_args *a, qp_stream_t stream) {
+namespace qp {
+
+int prefill_run(const qp_paged_cache *cache, const qp_prefill_args *a, const int32_t *skip_seq, hipStream_t s) {
   QP_REQUIRE(cache && a, "qp_prefill: null argument");
   QP_REQUIRE(cache->key.codes && cache->key.words && cache->value.codes && cache->value.words,
              "qp_prefill: null cache view");
@@ -864,10 +930,8 @@ extern "C" int qp_prefill(const qp_paged_cache *cache, const qp_prefill_args *a,
              "qp_prefill: query rows must be 16-byte aligned");
   QP_REQUIRE(aligned(a->out, 8) && a->out_stride[0] % 4 == 0 && a->out_stride[1] % 4 == 0,
              "qp_prefill: output rows must be 8-byte aligned");
-  QP_REQUIRE(!a->rht_signs || (a->out_stride[1] == hs && a->out_stride[0] == (int64_t)a->num_q_heads * hs),
-             "qp_prefill: the output rotation needs a contiguous output");
   if (a->num_seqs == 0 || a->num_tokens == 0) return QP_OK;
-  if (!mfma_prefill_shape(cache, a)) return slice_prefill(cache, a, reinterpret_cast<hipStream_t>(stream));
+  if (!mfma_prefill_shape(cache, a)) return slice_prefill(cache, a, skip_seq, s);
   int nt, bq;
   prefill_geometry(G, a->max_query_len, &nt, &bq);
   int splits = prefill_splits(cache, a, bq);
@@ -920,11 +984,14 @@ extern "C" int qp_prefill(const qp_paged_cache *cache, const qp_prefill_args *a,
   p.bq = bq;
   div_magic((uint32_t)cache->block_size, &p.bs_magic, &p.bs_shift);
   p.scale_log2 = a->softmax_scale * kLog2e;
+  p.qsigns = a->query_signs;
+  p.osigns = splits == 1 ? a->rht_signs : nullptr;  // split partials are rotated back by the merge
+  p.out_scale = a->rht_out_scale;
+  p.skip_seq = skip_seq;
   // sequence s owns query blocks [cu_q[s] / BQ + s, cu_q[s + 1] / BQ + s + 1): an upper bound known on the host
   const unsigned blocks = (unsigned)(a->num_tokens / bq + a->num_seqs);
   const dim3 grid(blocks, cache->num_kv_heads, splits);
   const bool span = is_span_layout(cache) && !getenv("QP_PREFILL_ROWS");
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (hs == 256) {
     if (cache->key.format == QP_CODES_INT4) dispatch_nt<256, QP_CODES_INT4>(p, nt, grid, span, s);
     else dispatch_nt<256, QP_CODES_INT8>(p, nt, grid, span, s);
@@ -956,10 +1023,13 @@ extern "C" int qp_prefill(const qp_paged_cache *cache, const qp_prefill_args *a,
     m.out_stride[1] = a->out_stride[1];
     m.rht_signs = a->rht_signs;
     m.rht_out_scale = a->rht_out_scale;
-    return qp_merge_segments(&m, stream);
+    return merge_routed(&m, nullptr, nullptr, 0, skip_seq, s);
   }
-  if (a->rht_signs)
-    return qp_rht(a->out, QP_DTYPE_BF16, hs, a->out, QP_DTYPE_BF16, hs, (int64_t)a->num_tokens * a->num_q_heads, hs,
-                  a->rht_signs, 1, a->rht_out_scale, stream);
   return QP_OK;
+}
+
+}  // namespace qp
+
+extern "C" int qp_prefill(const qp_paged_cache *cache, const qp_prefill_args *a, qp_stream_t stream) {
+  return prefill_run(cache, a, nullptr, reinterpret_cast<hipStream_t>(stream));
 }

@@ -41,7 +41,7 @@ class DecodeArgs(Structure):
                 ("num_tokens", c_int32), ("num_q_heads", c_int32), ("max_query_len", c_int32),
                 ("num_segments", c_int32), ("softmax_scale", c_float), ("segm_output", c_void_p),
                 ("segm_output_stride", I64x3), ("segm_max", c_void_p), ("segm_expsum", c_void_p),
-                ("segm_stat_stride", I64x2), ("segm_rows", c_int32)]
+                ("segm_stat_stride", I64x2), ("segm_rows", c_int32), ("query_signs", c_void_p)]
 
 
 class MergeArgs(Structure):
@@ -58,7 +58,19 @@ class PrefillArgs(Structure):
                 ("num_tokens", c_int32), ("num_q_heads", c_int32), ("max_query_len", c_int32),
                 ("max_seqlen_k", c_int32), ("num_splits", c_int32), ("softmax_scale", c_float), ("out", c_void_p),
                 ("out_stride", I64x2), ("workspace", c_void_p), ("workspace_bytes", c_int64),
-                ("rht_signs", c_void_p), ("rht_out_scale", c_float)]
+                ("rht_signs", c_void_p), ("rht_out_scale", c_float), ("query_signs", c_void_p)]
+
+
+class AttentionArgs(Structure):
+    _fields_ = [("query", c_void_p), ("query_stride", I64x2), ("cu_seqlens_q", c_void_p), ("seqused_k", c_void_p),
+                ("block_table", c_void_p), ("block_table_stride", c_int64), ("num_seqs", c_int32),
+                ("num_tokens", c_int32), ("num_q_heads", c_int32), ("max_query_len", c_int32),
+                ("max_seqlen_k", c_int32), ("softmax_scale", c_float), ("out", c_void_p), ("out_stride", I64x2),
+                ("segm_output", c_void_p), ("segm_output_stride", I64x3), ("segm_max", c_void_p),
+                ("segm_expsum", c_void_p), ("segm_stat_stride", I64x2), ("segm_rows", c_int32),
+                ("num_segments", c_int32), ("max_decode_rows", c_int32), ("rht_signs", c_void_p),
+                ("rht_out_scale", c_float),
+                ("workspace", c_void_p), ("workspace_bytes", c_int64)]
 
 
 class StoreArgs(Structure):
@@ -74,6 +86,8 @@ SIGNATURES = {
     "qp_merge_segments": (c_int32, [POINTER(MergeArgs), c_void_p]),
     "qp_prefill": (c_int32, [POINTER(PagedCache), POINTER(PrefillArgs), c_void_p]),
     "qp_prefill_workspace_size": (c_int64, [POINTER(PagedCache), POINTER(PrefillArgs)]),
+    "qp_attention": (c_int32, [POINTER(PagedCache), POINTER(AttentionArgs), c_void_p]),
+    "qp_attention_workspace_size": (c_int64, [POINTER(PagedCache), POINTER(AttentionArgs)]),
     "qp_store": (c_int32, [POINTER(PagedCache), POINTER(StoreArgs), c_void_p]),
     "qp_rht": (c_int32, [c_void_p, c_int32, c_int64, c_void_p, c_int32, c_int64, c_int64, c_int32, c_void_p,
                          c_int32, c_float, c_void_p]),

@@ -49,11 +49,12 @@ def _cu_seqlens(length: int, device) -> torch.Tensor:
 
 def prefill_attention(q, k_cache, v_cache, k_scale_cache, v_scale_cache, out, *, cu_seqlens_q, seqused_k,
                       block_table, max_seqlen_q, softmax_scale, max_seqlen_k=None, num_splits=0, rht_signs=None,
-                      rht_out_scale=1.0) -> None:
+                      rht_out_scale=1.0, query_signs=None) -> None:
     """Batched causal attention of the query tokens of every sequence (the last cu_seqlens_q[i+1] - cu_seqlens_q[i]
     positions of a context of seqused_k[i] tokens) over the paged cache: q and out bf16 [T, NQ, hs] in the cache's
     domain, softmax_scale multiplies q.k in that domain. With rht_signs the result is rotated back,
-    out = (o H D) * rht_out_scale. When the chunk alone cannot fill the GPU, the keys are split over workgroups
+    out = (o H D) * rht_out_scale; with query_signs q is unrotated and each row is rotated, (q D) H, as it loads.
+    When the chunk alone cannot fill the GPU, the keys are split over workgroups
     (num_splits, 0 = automatic) and merged; the fp32 partials go to a workspace from torch's caching allocator.
     max_seqlen_k bounds the automatic split count; without it the block table's capacity stands in (no host sync).
     Head 512, or more than 12 query heads per KV head, runs the split-KV decode kernel over causal query slices of
@@ -80,6 +81,7 @@ def prefill_attention(q, k_cache, v_cache, k_scale_cache, v_scale_cache, out, *,
     args.out_stride = _hip.I64x2(out.stride(0), out.stride(1))
     args.rht_signs = _hip.ptr(rht_signs)
     args.rht_out_scale = float(rht_out_scale)
+    args.query_signs = _hip.ptr(query_signs)
     lib = _hip.lib()
     need = lib.qp_prefill_workspace_size(cache, args)
     ws = torch.empty(need, dtype=torch.uint8, device=q.device) if need > 0 else None

@@ -10,10 +10,13 @@ is `qp_store` with an int8 key half.
 """
 from __future__ import annotations
 
+import dataclasses
+
 import torch
 
 from .. import _hip
 from . import rht
+from .vllm_hooks import HOOKS, Hook, find
 
 NAME = "k8v4_per_token_head"
 SCALE_BYTES = 4
@@ -92,74 +95,84 @@ def store(stock, key, value, key_cache, value_cache, slot_mapping, *, k_scale_ca
     _hip.check(_hip.lib().qp_store(cache, args, _hip.stream_of(key)), "reshape_and_cache_int4")
 
 
+def dtype_handler(int4_mode):
+    """The dtype registry's entry for k8v4: int8 storage (the int4 cache is uint8, which is how a spec or a cache view
+    tells the two formats apart where vLLM passes no dtype string) and the int4 per-token-head quantisation mode, so
+    that vLLM's per-token-head code paths (dynamic scales, the Triton backend, the packed dispatch) serve it."""
+    return type("K8v4Dtype", (), {"name": NAME, "torch_dtype": lambda self: torch.int8,
+                                  "quant_mode": lambda self: int4_mode})
+
+
 def register_dtype(logger) -> bool:
     """Make `--kv-cache-dtype k8v4_per_token_head` a valid vLLM option through its KV-cache dtype registry
     (k8v4_kv.py:89-110). False on a vLLM without the registry."""
     try:
-        from vllm.config import cache as cache_config
-        from vllm.v1.kv_cache_interface import KVQuantMode
-        registry, lookup = cache_config.register_kv_cache_dtype, cache_config.get_kv_cache_dtype_handler
-        mode = KVQuantMode.INT4_PER_TOKEN_HEAD
+        _, register, lookup = find("vllm.config.cache", "register_kv_cache_dtype", "get_kv_cache_dtype_handler")
+        _, int4_mode = find("vllm.v1.kv_cache_interface", "KVQuantMode.INT4_PER_TOKEN_HEAD")
     except Exception as e:
-        logger.debug("vllm-quantpack: %s not registered (%s)", NAME, e)
+        logger.debug("vllm-quantpack: no KV-cache dtype registry for %s (%s)", NAME, e)
         return False
     if lookup(NAME) is None:
-        class Handler:
-            name = NAME
-
-            def torch_dtype(self):
-                return torch.int8           # int8 storage tells the k8v4 cache apart from uint8 int4
-
-            def quant_mode(self):
-                return mode
-
-        registry(NAME)(Handler)
+        register(NAME)(dtype_handler(int4_mode))
     return True
 
 
-def patch_backend(stock, logger) -> bool:
-    """Teach vLLM's Triton backend the k8v4 cell and views (k8v4_kv.py:113-166): the spec's cell size, the key /
-    value / scale views of a k8v4 cache. The store and attention themselves are installed by int4_kv.patch_int4_kv."""
-    try:
-        from vllm.v1.attention.backends import triton_attn
-        from vllm.v1.kv_cache_interface import KVQuantMode
-        backend, impl = triton_attn.TritonAttentionBackend, triton_attn.TritonAttentionImpl
-        stock_spec = backend.customize_spec.__func__
-        stock_scales, stock_views = impl._ensure_scale_caches, impl._pth_key_value_caches
-        supported = backend.supported_kv_cache_dtypes
-    except Exception as e:
-        logger.warning("vllm-quantpack: %s not available on this vLLM (%s)", NAME, e)
-        return False
-    if getattr(stock_views, "_quantpack", False):
-        return True
+def backend_hooks(triton_attn, int4_mode) -> list:
+    """The Triton backend's knowledge of the k8v4 cell: the spec's cell size, and the key / value / scale views the
+    attention implementation takes from a layer's byte cache (k8v4_kv.py:113-166). Every other cache dtype is left
+    to vLLM's own methods."""
+    backend, impl = triton_attn.TritonAttentionBackend, triton_attn.TritonAttentionImpl
+    vllm_spec = backend.customize_spec.__func__
+    vllm_scales, vllm_views = impl._ensure_scale_caches, impl._pth_key_value_caches
+
+    def k8v4_spec(spec) -> bool:
+        return spec.state_content_bytes is None and spec.kv_quant_mode == int4_mode and spec.dtype == torch.int8
 
     def customize_spec(cls, spec):
-        if (spec.state_content_bytes is None and spec.kv_quant_mode == KVQuantMode.INT4_PER_TOKEN_HEAD
-                and spec.dtype == torch.int8):
-            from dataclasses import replace
-            return replace(spec, state_content_bytes=cell_bytes(spec.head_size, spec.head_size_v))
-        return stock_spec(cls, spec)
+        if not k8v4_spec(spec):
+            return vllm_spec(cls, spec)
+        return dataclasses.replace(spec, state_content_bytes=cell_bytes(spec.head_size, spec.head_size_v))
+
+    def k8v4_views(self, kv_cache):
+        """(key, value) views of a k8v4 layer cache; its two scale views go to the layer on first use, every scale
+        at 1.0 as vLLM starts per-token-head scales."""
+        key, value, k_scales, v_scales = views(kv_cache, self.head_size)
+        if self._k_scale_cache is None:
+            k_scales.fill_(1.0)
+            v_scales.fill_(1.0)
+            self._k_scale_cache, self._v_scale_cache = k_scales, v_scales
+        return key, value
 
     def _ensure_scale_caches(self, kv_cache):
         if self.kv_cache_dtype != NAME:
-            return stock_scales(self, kv_cache)
-        if self._k_scale_cache is None:
-            _, _, ks, vs = views(kv_cache, self.head_size)
-            ks.fill_(1.0)
-            vs.fill_(1.0)
-            self._k_scale_cache, self._v_scale_cache = ks, vs
+            return vllm_scales(self, kv_cache)
+        k8v4_views(self, kv_cache)
 
     def _pth_key_value_caches(self, kv_cache):
-        if self.kv_cache_dtype != NAME:
-            return stock_views(self, kv_cache)
-        self._ensure_scale_caches(kv_cache)
-        key, value, _, _ = views(kv_cache, self.head_size)
-        return key, value
+        return k8v4_views(self, kv_cache) if self.kv_cache_dtype == NAME else vllm_views(self, kv_cache)
 
-    _pth_key_value_caches._quantpack = True
-    backend.customize_spec = classmethod(customize_spec)
-    impl._ensure_scale_caches = _ensure_scale_caches
-    impl._pth_key_value_caches = _pth_key_value_caches
-    if NAME not in supported:
-        supported.append(NAME)
+    dtypes = list(backend.supported_kv_cache_dtypes)
+    return [Hook(backend, "customize_spec", classmethod(customize_spec), "k8v4 cell size in the attention spec"),
+            Hook(impl, "_ensure_scale_caches", _ensure_scale_caches, "k8v4 scale views"),
+            Hook(impl, "_pth_key_value_caches", _pth_key_value_caches, "k8v4 key / value views"),
+            Hook(backend, "supported_kv_cache_dtypes", dtypes + [NAME] if NAME not in dtypes else dtypes,
+                 "k8v4 among the backend's cache dtypes")]
+
+
+def patch_backend(stock, logger) -> bool:
+    """Install backend_hooks into vLLM's Triton backend. The store and the attention themselves are attached by
+    int4_kv.patch_int4_kv (the reference installs its k8v4 store here, k8v4_kv.py:145-166; `stock` is accepted for
+    that call signature). False on a vLLM without the backend methods or the int4 quantisation mode."""
+    del stock
+    try:
+        triton_attn, _, _, _ = find("vllm.v1.attention.backends.triton_attn", "TritonAttentionBackend.customize_spec",
+                                    "TritonAttentionImpl._ensure_scale_caches",
+                                    "TritonAttentionImpl._pth_key_value_caches")
+        _, int4_mode = find("vllm.v1.kv_cache_interface", "KVQuantMode.INT4_PER_TOKEN_HEAD")
+        hooks = backend_hooks(triton_attn, int4_mode)
+    except Exception as e:
+        logger.warning("vllm-quantpack: %s not available on this vLLM (%s)", NAME, e)
+        return False
+    for hook in hooks:
+        HOOKS.apply(hook)
     return True

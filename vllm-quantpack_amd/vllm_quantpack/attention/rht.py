@@ -29,13 +29,33 @@ def signs_np(head_size: int, seed: int = 0) -> np.ndarray:
     return np.where(x & np.uint64(1), -1.0, 1.0).astype(np.float32)
 
 
+def _signs_on(head_size: int, device: torch.device, seed: int) -> torch.Tensor:
+    """signs_np computed by kernels on `device` (an arange and integer arithmetic), so that no host buffer is copied
+    and the host never waits: the int64 products keep their low 32 bits exact, which is all the hash uses."""
+    x = (torch.arange(head_size, dtype=torch.int64, device=device) + seed * 0x9E3779B9) & 0xFFFFFFFF
+    x = x ^ (x >> 16)
+    x = (x * 0x7FEB352D) & 0xFFFFFFFF
+    x = x ^ (x >> 15)
+    x = (x * 0x846CA68B) & 0xFFFFFFFF
+    x = x ^ (x >> 16)
+    return 1.0 - 2.0 * (x & 1).to(torch.float32)
+
+
 def signs(head_size: int, device, seed: int = 0) -> torch.Tensor:
-    """The diagonal D as an fp32 device tensor (cached per device, head size and seed)."""
+    """The diagonal D as an fp32 device tensor, cached per device, head size and seed. Made on the device without a
+    host copy; inside a HIP-graph capture only a cached tensor can be returned (kernels recorded there would not run
+    before the capture ends), so callers that capture create it first (patch_int4_kv does, for the usual head
+    sizes)."""
     device = torch.device(device)
+    if device.type == "cuda" and device.index is None:
+        device = torch.device("cuda", torch.cuda.current_device())
     key = (device, head_size, seed)
     t = _SIGNS.get(key)
     if t is None:
-        t = torch.from_numpy(signs_np(head_size, seed)).to(device)
+        if device.type == "cuda" and torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(f"rht.signs({head_size}) first requested during a HIP-graph capture: create it before "
+                               "capturing (vllm_quantpack.attention.rht.signs or patch_int4_kv)")
+        t = _signs_on(head_size, device, seed)
         _SIGNS[key] = t
     return t
 
