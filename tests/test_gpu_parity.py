@@ -244,16 +244,14 @@ def test_merge_lse_matches_the_oracle(device, fmt, lens, segments):
     cu = np.concatenate(([0], np.cumsum(Ts))).astype(np.int32)
     lse = torch.full((sum(Ts), NQ), float("nan"), dtype=torch.float32, device=device)
     out = torch.empty((sum(Ts), NQ, HS), dtype=torch.bfloat16, device=device)
+    cu_t, used_t = i32(cu, device), i32([n for _, n in lens], device)   # held until the merge has run
     margs = int4_kv._hip.MergeArgs(so.data_ptr(), int4_kv._hip.I64x3(*so.stride()[:3]), sm.data_ptr(),
-                                   ss.data_ptr(), int4_kv._hip.I64x2(sm.stride(0), sm.stride(1)),
-                                   i32(cu, device).data_ptr(), i32([n for _, n in lens], device).data_ptr(),
-                                   len(lens), sum(Ts), NQ, HS, segments, out.data_ptr(),
+                                   ss.data_ptr(), int4_kv._hip.I64x2(sm.stride(0), sm.stride(1)), cu_t.data_ptr(),
+                                   used_t.data_ptr(), len(lens), sum(Ts), NQ, HS, segments, out.data_ptr(),
                                    int4_kv._hip.I64x2(out.stride(0), out.stride(1)), lse.data_ptr(),
                                    int4_kv._hip.I64x2(lse.stride(0), lse.stride(1)), None, 1.0)
-    keep = (cu, lens)
     int4_kv._hip.check(int4_kv._hip.lib().qp_merge_segments(margs, int4_kv._hip.stream_of(out)), "merge")
     torch.cuda.synchronize()
-    del keep
     got = to_f32(lse)
     scale = HS ** -0.5
     for i, (T, n) in enumerate(lens):
