@@ -217,6 +217,21 @@ int qp_attention(const qp_paged_cache *cache, const qp_attention_args *args, qp_
 int64_t qp_attention_workspace_size(const qp_paged_cache *cache, const qp_attention_args *args);
 
 /*
+ * qp_attention for a batch of short sequences (a decode / MTP-verify step: max_query_len <= QP_DECODE_MAX_QUERY and
+ * at most 32 query rows per KV head) that allocates nothing and takes no scratch from the caller: the split-KV
+ * partials live in the library's own device buffer of QP_NOALLOC_SCRATCH_BYTES, one per GPU, kept until the process
+ * ends. args->segm_output / segm_max / segm_expsum / segm_rows and the workspace are not read; num_segments is.
+ * A batch whose partials (num_tokens x num_q_heads x num_segments x (head_size + 2) x 4 bytes) exceed the buffer, or
+ * that is not a batch of short sequences, is rejected with QP_ERR_UNSUPPORTED before anything runs.
+ * Every call on one GPU shares that GPU's buffer and leaves its partials there: calls that overlap on one GPU (two
+ * streams, two host threads) race and must be ordered by the caller.
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under HIP-graph capture
+ * without a pool, tight serving loops, harnesses that forbid allocation).
+ */
+#define QP_NOALLOC_SCRATCH_BYTES (32ll << 20)
+int qp_attention_noalloc(const qp_paged_cache *cache, const qp_attention_args *args, qp_stream_t stream);
+
+/*
  * Quantise-and-store of new keys/values into the paged cache: per (token, KV head) keys to int4 (asymmetric
  * min/max, zero point in the scale word) or int8 (absmax / 127), values to int4; token i goes to slot
  * slot_mapping[i], negative slots are skipped. Optional rht_signs rotate key and value first (x -> x D H^T).

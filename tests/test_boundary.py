@@ -26,7 +26,7 @@ def _declared():
 def test_header_declares_the_entry_points():
     assert _declared() == sorted(["qp_unpack_segment", "qp_decode_splitkv", "qp_merge_segments", "qp_prefill",
                                   "qp_prefill_workspace_size", "qp_attention", "qp_attention_workspace_size",
-                                  "qp_store", "qp_rht", "qp_last_error", "qp_version"])
+                                  "qp_attention_noalloc", "qp_store", "qp_rht", "qp_last_error", "qp_version"])
 
 
 def test_library_loads_and_exports_every_declared_symbol():

@@ -13,6 +13,8 @@
 // and the merge / the prefill epilogue rotate the output back before the one bf16 store.
 #include "qp_common.h"
 
+#include <mutex>
+
 namespace qp {
 
 // One workgroup. route_row[i]: first segment-buffer row of short sequence i, -1 for the others (and for short ones
@@ -224,4 +226,83 @@ extern "C" int qp_attention(const qp_paged_cache *cache, const qp_attention_args
   m.rht_signs = a->rht_signs;
   m.rht_out_scale = a->rht_out_scale;
   return merge_routed(&m, row_tok, row_seq, P.rows_cap, nullptr, s);
+}
+
+// ------------------------------------------------------------------------------ entry point without allocation
+//
+// The split-KV partials of qp_attention_noalloc live in this file-scope device array: one copy per GPU the library
+// runs on, held until the process ends. Host code never passes `scratch` itself to a kernel (in host code the name
+// stands for a host-side shadow, not a device address): each device's address comes from hipGetSymbolAddress, taken
+// once per device with that device current, and only that pointer is used.
+static __device__ __align__(256) uint8_t scratch[QP_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up on the device's first call.
+int scratch_on_current_device(void **ptr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail((int)e, std::string("qp_attention_noalloc: hipGetDevice: ") + hipGetErrorString(e));
+  QP_SUPPORTED(dev >= 0 && dev < kMaxDevices, "qp_attention_noalloc: device index beyond 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(e != hipSuccess ? (int)e : QP_ERR_INVALID,
+                  std::string("qp_attention_noalloc: hipGetSymbolAddress: ") + hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return QP_OK;
+}
+
+}  // namespace
+
+extern "C" int qp_attention_noalloc(const qp_paged_cache *cache, const qp_attention_args *args, qp_stream_t stream) {
+  QP_REQUIRE(cache && args, "qp_attention_noalloc: null argument");
+  QP_REQUIRE(args->num_seqs >= 0 && args->num_tokens >= 0 && args->num_q_heads > 0 && cache->num_kv_heads > 0 &&
+                 args->num_q_heads % cache->num_kv_heads == 0,
+             "qp_attention_noalloc: bad sizes");
+  const int hs = cache->head_size;
+  const int G = args->num_q_heads / cache->num_kv_heads;
+  QP_SUPPORTED(args->max_query_len >= 1 && args->max_query_len <= QP_DECODE_MAX_QUERY &&
+                   args->max_query_len * G <= 32,
+               "qp_attention_noalloc: only batches of sequences with 1..4 query tokens and at most 32 query rows per "
+               "KV head (a decode step)");
+  QP_SUPPORTED(hs == 128 || hs == 256 || hs == 512, "qp_attention_noalloc: head size must be 128, 256 or 512");
+  QP_REQUIRE(args->num_segments >= 1 && args->num_segments <= 2048, "qp_attention_noalloc: 1..2048 segments");
+  // [segment rows: tokens x heads x segments x head_size | maxima | sums], fp32, each part 256-byte aligned
+  const int64_t triples = (int64_t)args->num_tokens * args->num_q_heads * args->num_segments;
+  const int64_t rows_bytes = (triples * hs * 4 + 255) / 256 * 256;
+  const int64_t stat_bytes = (triples * 4 + 255) / 256 * 256;
+  const int64_t need = rows_bytes + 2 * stat_bytes;
+  if (need > QP_NOALLOC_SCRATCH_BYTES)
+    return fail(QP_ERR_UNSUPPORTED, "qp_attention_noalloc: the batch's split-KV partials need " + std::to_string(need) +
+                                        " bytes, more than the " + std::to_string(QP_NOALLOC_SCRATCH_BYTES) +
+                                        "-byte static buffer (fewer segments, or qp_attention with caller buffers)");
+  if (args->num_seqs == 0 || args->num_tokens == 0) return QP_OK;
+  void *base = nullptr;
+  const int st = scratch_on_current_device(&base);
+  if (st != QP_OK) return st;
+  qp_attention_args a = *args;
+  float *rows = static_cast<float *>(base);
+  a.segm_output = rows;
+  a.segm_output_stride[2] = hs;
+  a.segm_output_stride[1] = (int64_t)args->num_segments * hs;
+  a.segm_output_stride[0] = (int64_t)args->num_q_heads * a.segm_output_stride[1];
+  a.segm_max = reinterpret_cast<float *>(static_cast<uint8_t *>(base) + rows_bytes);
+  a.segm_expsum = reinterpret_cast<float *>(static_cast<uint8_t *>(base) + rows_bytes + stat_bytes);
+  a.segm_stat_stride[1] = args->num_segments;
+  a.segm_stat_stride[0] = (int64_t)args->num_q_heads * args->num_segments;
+  a.segm_rows = args->num_tokens;
+  a.workspace = nullptr;
+  a.workspace_bytes = 0;
+  // a batch of short sequences whose rows all fit: qp_attention's decode + merge, which needs no workspace
+  QP_REQUIRE(qp_attention_workspace_size(cache, &a) == 0, "qp_attention_noalloc: not a batch of short sequences");
+  return qp_attention(cache, &a, stream);
 }

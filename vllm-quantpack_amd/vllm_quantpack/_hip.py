@@ -88,6 +88,7 @@ SIGNATURES = {
     "qp_prefill_workspace_size": (c_int64, [POINTER(PagedCache), POINTER(PrefillArgs)]),
     "qp_attention": (c_int32, [POINTER(PagedCache), POINTER(AttentionArgs), c_void_p]),
     "qp_attention_workspace_size": (c_int64, [POINTER(PagedCache), POINTER(AttentionArgs)]),
+    "qp_attention_noalloc": (c_int32, [POINTER(PagedCache), POINTER(AttentionArgs), c_void_p]),
     "qp_store": (c_int32, [POINTER(PagedCache), POINTER(StoreArgs), c_void_p]),
     "qp_rht": (c_int32, [c_void_p, c_int32, c_int64, c_void_p, c_int32, c_int64, c_int64, c_int32, c_void_p,
                          c_int32, c_float, c_void_p]),
