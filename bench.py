@@ -8,8 +8,10 @@ cache), so each step reads its cache from HBM rather than from the last-level ca
 
 Prints one JSON line: decode tok/s (value), HBM GB/s and us per layer, the prefill-chunk workload's tok/s when the
 prefill kernel is available, the roofline of the decode kernel (algorithmic bytes / its average duration measured with
-events on its stream around a run of launches queued behind a spin, so the events see execution only) and the CPU
-baseline (the dequantise-then-attend restatement timed on this host).
+events on its stream around a run of launches queued behind a spin, so the events see execution only), the drop-in
+path's time per layer (unified_attention_int4 with the query rotation, eager and as a graph replay) and the CPU
+baselines (the dequantise-then-attend restatement timed on this host, on the decode step and on a sample of the
+prefill chunk).
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--segments N] [--no-cpu] [--no-prefill]
     python bench.py --copy-probe MIB     # only a plain device copy of MIB MiB, 10 times (HBM counter calibration)
@@ -81,8 +83,67 @@ def decode_bench(torch, args):
     kern_ms = a.elapsed_time(b) / args.steps
     nbytes = synth.cache_bytes(w)
     result = dict(tokens_per_step=T, step_ms=step_ms, decode_kernel_us=kern_ms * 1e3, bytes=nbytes, segments=S,
-                  out=out, w=w)
+                  out=out, w=w, copies=copies)
     return result
+
+
+def dropin_bench(torch, args, r):
+    """The drop-in path of one layer: unified_attention_int4 on unrotated queries (the query rotation, split-KV
+    decode, merge and inverse rotation in one qp_attention call, plus the Python layer's argument checks and
+    ctypes structs), timed eagerly over `steps` calls and as `steps` replays of one captured HIP graph."""
+    from vllm_quantpack.attention import int4_kv, rht
+    from vllm_quantpack.tools import synth
+    dev = torch.device("cuda:0")
+    w = r["w"]
+    d = r["copies"][0]
+    copies = r["copies"]
+    T, NQ, HS = w.q.shape
+    S = r["segments"]
+    segm = (torch.empty((T, NQ, S, HS), dtype=torch.float32, device=dev),
+            torch.empty((T, NQ, S), dtype=torch.float32, device=dev),
+            torch.empty((T, NQ, S), dtype=torch.float32, device=dev))
+    out = torch.empty((T, NQ, HS), dtype=torch.bfloat16, device=dev)
+    rht.signs(HS, dev)
+
+    def layer(c):
+        int4_kv.unified_attention_int4(
+            c["q"], c["k_cache"], c["v_cache"], out, cu_seqlens_q=c["cu_seqlens_q"], max_seqlen_q=w.max_query_len,
+            seqused_k=c["seqused_k"], max_seqlen_k=int(w.seqused_k.max()), softmax_scale=w.softmax_scale * HS,
+            window_size=(-1, -1), block_table=c["block_table"], softcap=0.0, sinks=None, alibi_slopes=None,
+            use_alibi_sqrt=False, qq_bias=None, output_scale=None, mm_prefix_range=None,
+            k_scale_cache=c["k_scale_cache"], v_scale_cache=c["v_scale_cache"], seq_threshold_3D=T,
+            num_par_softmax_segments=S, softmax_segm_output=segm[0], softmax_segm_max=segm[1],
+            softmax_segm_expsum=segm[2])
+
+    n = len(copies)
+    for i in range(args.warmup):
+        layer(copies[i % n])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        layer(copies[i % n])
+    torch.cuda.synchronize()
+    eager_us = (time.perf_counter() - t0) * 1e6 / args.steps
+    graphs = []
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for c in copies:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                layer(c)
+            graphs.append(g)
+    torch.cuda.synchronize()
+    for i in range(args.warmup):
+        graphs[i % n].replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        graphs[i % n].replay()
+    torch.cuda.synchronize()
+    graph_us = (time.perf_counter() - t0) * 1e6 / args.steps
+    del synth, d
+    return dict(eager_us=eager_us, graph_us=graph_us)
 
 
 def prefill_bench(torch, args):
@@ -142,6 +203,31 @@ def counted_traffic():
     return None
 
 
+def cpu_prefill_baseline(sample_tokens=128):
+    """The same dequantise-then-attend restatement on the prefill chunk workload, one rep over a bounded sample: the
+    first `sample_tokens` query tokens of the 1024-token chunk (each attending to the 131072 cached keys and the
+    chunk's tokens before it), reported as tokens per second of that sample."""
+    import torch
+
+    from oracle import qp_oracle as O
+    from vllm_quantpack.tools import synth
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    w = synth.make("prefill-int4-128k-c1024")
+    views = O.int4_views(w.kv, w.head_size)
+    # the chunk's own keys: the oracle store writes them as the workload's setup does on the device
+    O.store(views, O.bf16_bits_to_f32(w.new_key), O.bf16_bits_to_f32(w.new_value), w.new_slots)
+    n = int(w.seqused_k[0])
+    chunk = w.q.shape[0]
+    q = O.bf16_bits_to_f32(w.q[:sample_tokens])
+    t = time.perf_counter()
+    O.prefill_dequant_attend(q, views, w.block_table[0], n - chunk + sample_tokens, w.softmax_scale)
+    dt = time.perf_counter() - t
+    return dict(value=round(sample_tokens / dt, 2), unit="tok/s", cores=threads, kind="port",
+                sample=f"first {sample_tokens} query tokens of prefill-int4-128k-c1024 ({n - chunk} cached keys, "
+                       f"causal in the chunk), 1 rep, {dt:.2f} s, torch {torch.__version__} CPU")
+
+
 def cpu_baseline(w, budget_s=20.0):
     """The oracle's dequantise-then-attend restatement of the reference's path, on this host's cores."""
     import numpy as np
@@ -173,6 +259,7 @@ def main(argv=None):
     ap.add_argument("--segments", type=int, default=0, help="split-KV segments (default: sized for the CU count)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-chunk workload")
+    ap.add_argument("--no-dropin", action="store_true", help="skip the unified_attention_int4 (drop-in path) timing")
     ap.add_argument("--cache-copies", type=int, default=4,
                     help="copies of the decode cache used in turn (1: the cache stays in the last-level cache)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB", help="only run a plain copy of MIB MiB")
@@ -215,7 +302,9 @@ def main(argv=None):
         "hbm_gbps_decode_kernel": round(r["bytes"] / kern_s / 1e9, 1),
         "roofline": {"bound": "hbm", "achieved": round(r["bytes"] / kern_s / 1e9, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(r["bytes"] / kern_s / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": counted_traffic(), "kernel": DECODE_KERNEL,
+                     "traffic": counted_traffic(), "traffic_source": "FETCH_SIZE + WRITE_SIZE counters of the "
+                     "committed summary profiles/decode_span_kernel_decode-int4-128k-t2_traffic.txt (not this run)",
+                     "kernel": DECODE_KERNEL,
                      "bytes_per_launch": r["bytes"], "avg_us": round(r["decode_kernel_us"], 2)},
     }
     if not args.no_prefill:
@@ -226,9 +315,16 @@ def main(argv=None):
                                "mfma_frac": round(p["tflops"] / BF16_PEAK_TFLOPS, 4)}
         except NotImplementedError as e:
             line["prefill"] = {"workload": "prefill-int4-128k-c1024", "tok_s": None, "note": str(e)}
+    if not args.no_dropin:
+        dr = dropin_bench(torch, args, r)
+        line["dropin"] = {"what": "unified_attention_int4 per layer on unrotated queries (rotation fused)",
+                          "eager_us_per_layer": round(dr["eager_us"], 2), "graph_us_per_layer": round(dr["graph_us"], 2)}
+        log(f"drop-in layer: {dr['eager_us']:.1f} us eager, {dr['graph_us']:.1f} us graph replay")
     if not args.no_cpu:
         log("CPU baseline ...")
         line["cpu_baseline"] = cpu_baseline(r["w"])
+        if not args.no_prefill:
+            line["cpu_baseline_prefill"] = cpu_prefill_baseline()
     print(json.dumps(line), flush=True)
     return 0
 

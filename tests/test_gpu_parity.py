@@ -630,7 +630,8 @@ def test_prefill_key_splits_agree(device, splits):
 @pytest.mark.parametrize("fmt", ["int4", "int8"])
 def test_prefill_scores_far_above_the_first_tile(device, fmt):
     """Keys with scales 2^7 .. 2^12 late in the context push scores thousands of log2 units above the first tile's
-    maximum: the workgroup raises its maximum and redoes its keys, and the result still matches."""
+    maximum: each row raises its maximum where the scores exceed it, scaling its sum and accumulators down in place
+    (by assembly on the AGPR tiles), and the result still matches."""
     rng = np.random.default_rng(211)
     big = [(700, 2.0 ** 7), (1300, 2.0 ** 9), (1901, 2.0 ** 12)]
     out, emu, ref = _prefill_case(device, rng, fmt, [(40, 2000), (9, 1400)], splits=1, big_keys=big)

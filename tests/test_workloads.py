@@ -13,6 +13,7 @@ from oracle import qp_oracle as O
 from qp_testlib import assert_emulation, to_f32
 
 DECODE = ["decode-int4-4k-t1", "decode-int4-128k-t2", "decode-int4-256k-t4", "decode-k8v4-ragged-b32"]
+PREFILL = ["prefill-int4-128k-c1024", "prefill-k8v4-128k-c1024"]
 SEGMENTS = 64
 
 
@@ -86,9 +87,10 @@ def test_small_decode_workloads_match_the_oracle(device, name):
 
 
 @pytest.mark.gpu
-def test_small_prefill_workload_matches_the_oracle(device):
+@pytest.mark.parametrize("name", PREFILL)
+def test_small_prefill_workload_matches_the_oracle(device, name):
     from vllm_quantpack.tools import synth
-    w = synth.make("prefill-int4-128k-c1024", small=True)
+    w = synth.make(name, small=True)
     out, _ = _prefill(w, device)
     # the oracle stores the chunk's keys the same way, then attends in fp64
     views = _views(w)
@@ -174,9 +176,10 @@ def test_full_size_decode_workloads_match_fp64(device, name):
 
 
 @pytest.mark.gpu
-def test_full_size_prefill_workload_matches_fp64(device):
+@pytest.mark.parametrize("name", PREFILL)
+def test_full_size_prefill_workload_matches_fp64(device, name):
     from vllm_quantpack.tools import synth
-    w = synth.make("prefill-int4-128k-c1024")
+    w = synth.make(name)
     out, d = _prefill(w, device)          # the cache on the device now holds the stored chunk
     ref = _full_reference(w, d)
     assert np.isfinite(out).all()

@@ -334,4 +334,26 @@ __device__ __forceinline__ void table_pair(const int32_t *trow, int i0, int i1, 
 #endif
 }
 
+// acc[0 .. USED) *= alpha on AGPR tiles, one tile at a time through the lane's 16 bytes of LDS at rs. Tiles move
+// between the AGPRs and LDS only inside assembly blocks (LDS loads and stores take AGPR data): any C++ access to an
+// element makes the register allocator keep a VGPR copy of every tile and refresh it at each chunk, although the
+// rescale runs only a few times per segment. Callers run it at least 18 wait states after the last accumulation into
+// the tiles (the last inline MFMA of a chunk ends with them); the lgkm wait at its end completes the reload before any
+// later MFMA reads a tile.
+template <int N, int USED = N>
+__device__ __forceinline__ void scale_agpr(f32x4_t (&acc)[N], float alpha, f32x4_t *rs) {
+  const uint32_t at = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) f32x4_t *)rs;
+#pragma unroll
+  for (int i = 0; i < USED; ++i) {
+    asm volatile("ds_write_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" ::"v"(at), "a"(acc[i]) : "memory");
+    f32x4_t t = *reinterpret_cast<volatile f32x4_t *>(rs);
+    t[0] *= alpha;
+    t[1] *= alpha;
+    t[2] *= alpha;
+    t[3] *= alpha;
+    *reinterpret_cast<volatile f32x4_t *>(rs) = t;
+    asm volatile("s_waitcnt lgkmcnt(0)\n\tds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=a"(acc[i]) : "v"(at) : "memory");
+  }
+}
+
 }  // namespace qp

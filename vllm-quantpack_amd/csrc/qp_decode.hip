@@ -303,27 +303,6 @@ __device__ __forceinline__ void pv_tile_agpr(f32x4_t (&acc)[NCT][N], int i, bf16
   }
 }
 
-// acc *= alpha on AGPR tiles, one tile at a time through the lane's 16 bytes of LDS at rs. Tiles move between the
-// AGPRs and LDS only inside assembly blocks (LDS loads and stores take AGPR data): any C++ access to an element makes
-// the register allocator keep a VGPR copy of every tile and refresh it at each chunk, although the rescale runs only a
-// few times per segment. The last accumulation reached this block at least 18 wait states earlier (the chunk's last
-// PV tile ends with them); the next one waits 2 after the reload (pv_tile_agpr), which the lgkm wait has completed.
-template <int N>
-__device__ __forceinline__ void scale_agpr(f32x4_t (&acc)[N], float alpha, f32x4_t *rs) {
-  const uint32_t at = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) f32x4_t *)rs;
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    asm volatile("ds_write_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" ::"v"(at), "a"(acc[i]) : "memory");
-    f32x4_t t = *reinterpret_cast<volatile f32x4_t *>(rs);
-    t[0] *= alpha;
-    t[1] *= alpha;
-    t[2] *= alpha;
-    t[3] *= alpha;
-    *reinterpret_cast<volatile f32x4_t *>(rs) = t;
-    asm volatile("s_waitcnt lgkmcnt(0)\n\tds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=a"(acc[i]) : "v"(at) : "memory");
-  }
-}
-
 // Softmax of the chunk and O^T += V^T P^T; fb: float4 of per-key scalars per key.
 template <int HS, int KFMT, int NCT>
 __device__ __forceinline__ void chunk_finish(WaveState<HS, KFMT, NCT> &st, const ChunkState<HS, NCT> &cr,

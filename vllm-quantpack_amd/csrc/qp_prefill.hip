@@ -4,7 +4,8 @@
 // Reference semantics: the reference routes long prefill chunks to FlashAttention over segments unpacked to bf16
 // (int4_prefill.py:203-232) and short ones to its exact Triton kernel (int4_kv.py:80-95, 113-118). This kernel
 // computes the exact kernel's arithmetic for any chunk length: bf16 query and exact-integer code operands, fp32
-// accumulation, S = (q . (128 + k) - sum(q) (128 + zp_k)) s_k scale, P_v16 = bf16(P s_v) feeding both the PV product
+// accumulation, S = (q . (128 + k) - sum(q) (128 + zp_k)) s_k scale for int4 keys and (q . (128 + k) - 128 sum(q))
+// s_k scale for int8 keys (both operands exact bf16 integers), P_v16 = bf16(P s_v) feeding both the PV product
 // and the zero-point sum (int4_kv.py:90-94), l from the unrounded P, causal within each sequence's query chunk.
 //
 // MI355X design. A workgroup of 4 waves (one per SIMD) owns (query block, KV head, key split). The query block holds
@@ -64,7 +65,6 @@ struct PrefillParams {
 constexpr int kPfKeys = 32;  // keys per tile
 constexpr int kPfWaves = 4;
 constexpr float kPfRescale = 64.f;  // log2 headroom before the running maximum is raised
-constexpr int kPfMaxPasses = 8;     // passes over a split's keys (restarts after a raised maximum) at most
 
 template <int HS, int KFMT>
 struct PfShape {
@@ -152,6 +152,15 @@ __device__ __forceinline__ void pf_gather(const PrefillParams &p, const int32_t 
   }
 }
 
+// Four int8 codes of a dword as bf16 integers 128 + k (1..255, exact): flipping the sign bits makes each byte the
+// unsigned 128 + k, which v_cvt_f32_ubyte0..3 converts directly. The +128 folds into the score through the key's e
+// scalar (128 a_k) and the row's query sum, as the int4 zero point does. Returns (channels 0,1) and (2,3).
+__device__ __forceinline__ u32x2_t i8_quad_bf16(uint32_t x) {
+  const uint32_t u = x ^ 0x80808080u;
+  return u32x2_t{pack_bf16x2((float)(u & 0xFFu), (float)((u >> 8) & 0xFFu)),
+                 pack_bf16x2((float)((u >> 16) & 0xFFu), (float)(u >> 24))};
+}
+
 // K part of the unpack: bf16 K rows kd[key][channel], 8 channels per dword of int4 codes (4 of int8).
 template <int HS, int KFMT>
 __device__ __forceinline__ void pf_unpack_k(const uint8_t *pk, uint8_t *kd, int tid) {
@@ -175,9 +184,7 @@ __device__ __forceinline__ void pf_unpack_k(const uint8_t *pk, uint8_t *kd, int 
       const int u = tid + kPfWaves * 64 * i;
       const int kk = u / kDw, d = u % kDw;
       const uint32_t x = *reinterpret_cast<const uint32_t *>(pk + kk * Sh::kCell + 4 * d);
-      const uint32_t lo = pack_bf16x2((float)(int8_t)(x & 0xFF), (float)(int8_t)((x >> 8) & 0xFF));
-      const uint32_t hi = pack_bf16x2((float)(int8_t)((x >> 16) & 0xFF), (float)(int8_t)(x >> 24));
-      *reinterpret_cast<u32x2_t *>(kd + kk * Sh::kKdRow + 8 * d) = u32x2_t{lo, hi};
+      *reinterpret_cast<u32x2_t *>(kd + kk * Sh::kKdRow + 8 * d) = i8_quad_bf16(x);
     }
   }
 }
@@ -216,12 +223,13 @@ __device__ __forceinline__ void pf_unpack_v(const uint8_t *pk, uint8_t *vt, int 
     const bool ok = k0 + kk < kend;
     const uint32_t kw = *reinterpret_cast<const uint32_t *>(pk + kk * Sh::kCell + Sh::kKeyBytes);
     const uint32_t vw = *reinterpret_cast<const uint32_t *>(pk + kk * Sh::kCell + Sh::kCell - 4);
-    float a, e = 0.f;
+    float a, e;
     if constexpr (KFMT == QP_CODES_INT4) {
       a = __uint_as_float(kw & 0xFFFFFFF0u) * scale_log2;
       e = a * (float)(128u + (kw & 0xFu));
     } else {
       a = __uint_as_float(kw) * scale_log2;
+      e = a * 128.f;  // the operands are 128 + k
     }
     float *kf = reinterpret_cast<float *>(vt + Sh::kVt);
     kf[kk] = ok ? a : 0.f;
@@ -268,9 +276,7 @@ struct PfStager {
       *reinterpret_cast<u32x4_t *>(kd + kk * Sh::kKdRow + 16 * d) =
           u32x4_t{nib_pair(x), nib_pair(y), nib_pair(x >> 8), nib_pair(y >> 8)};
     } else {
-      const uint32_t lo = pack_bf16x2((float)(int8_t)(x & 0xFF), (float)(int8_t)((x >> 8) & 0xFF));
-      const uint32_t hi = pack_bf16x2((float)(int8_t)((x >> 16) & 0xFF), (float)(int8_t)(x >> 24));
-      *reinterpret_cast<u32x2_t *>(kd + kk * Sh::kKdRow + 8 * d) = u32x2_t{lo, hi};
+      *reinterpret_cast<u32x2_t *>(kd + kk * Sh::kKdRow + 8 * d) = i8_quad_bf16(x);
     }
   }
   // V unit (q4, ko) = tid mod HS (with HS = 128 the upper half repeats the lower half's unit: same bytes, same place)
@@ -300,12 +306,13 @@ struct PfStager {
   __device__ __forceinline__ void s_store() {
     const int kk = tid & (kPfKeys - 1);
     const bool ok = k0 + kk < kend;
-    float a, e = 0.f;
+    float a, e;
     if constexpr (KFMT == QP_CODES_INT4) {
       a = __uint_as_float(kw & 0xFFFFFFF0u) * scale_log2;
       e = a * (float)(128u + (kw & 0xFu));
     } else {
       a = __uint_as_float(kw) * scale_log2;
+      e = a * 128.f;  // the operands are 128 + k
     }
     const bool own = tid < kPfKeys;
     float *kf = reinterpret_cast<float *>(vt + Sh::kVt);
@@ -402,8 +409,7 @@ __device__ __forceinline__ void pf_initial_max(PfRows<HS, NT> &r, const f32x4_t 
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         float v;
-        if constexpr (KFMT == QP_CODES_INT4) v = fmaf(sacc[j][sub][jj], a[jj], -(r.qsum[j] * e[jj]));
-        else v = sacc[j][sub][jj] * a[jj];
+        v = fmaf(sacc[j][sub][jj], a[jj], -(r.qsum[j] * e[jj]));
         const int key = k0 + 16 * sub + 4 * g + jj;
         if (masked && (key > r.row_pos[j] || key >= kend)) v = -INFINITY;
         rm = fmaxf(rm, v);
@@ -422,12 +428,13 @@ __device__ __forceinline__ void pf_initial_max(PfRows<HS, NT> &r, const f32x4_t 
 // Each phase is written as a sequence of MFMA steps, the operand loads three steps ahead and the VALU work spread
 // between them. The steps are not fenced: the compiler's own interleaving across steps measures 5 % faster than
 // sched_barrier fences after every step (4.09-4.15 against 4.37 ms on the 1024-token chunk over 131072 keys).
-// A score beyond the headroom only posts a restart request (the tile index) for the next barrier.
+// A row whose scores exceed the running maximum by more than the headroom raises its maximum there, in phase A: its
+// l and its accumulators are scaled down by the difference (rare; the tiles move through rescale_lds, a lane's 16 bytes
+// of an LDS region no wave reads during phase A), and the tile's probabilities are taken against the new maximum.
 template <int HS, int KFMT, int NT, bool MASK>
 __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev)[NT][2], f32x4_t (&snew)[NT][2],
                                         const uint8_t *kd1, const uint8_t *vb0, int k0, int kend,
-                                        int *restart, int it, bool may_restart, PfStager<HS, KFMT> &st, int col,
-                                        int g) {
+                                        f32x4_t *rescale_lds, PfStager<HS, KFMT> &st, int col, int g) {
   using Sh = PfShape<HS, KFMT>;
   using St = PfStager<HS, KFMT>;
   constexpr int kMi = HS / 32;     // 32-channel steps per 16-key sub-tile
@@ -435,16 +442,16 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
   constexpr int kP = HS / 16 + 1;  // V^T operands (channel tiles + the zero-point tile)
   constexpr int kPre = 3;
   constexpr int kSm = 7;           // softmax work items per row tile
-  static_assert(St::kNK * 2 <= kQ, "K unpack stages must fit phase A");
+  constexpr int kLag = St::kNK < 4 ? St::kNK : 4;
+  static_assert(St::kNK + kLag <= kQ, "K unpack stages must fit phase A");
   const float *kf = reinterpret_cast<const float *>(vb0 + Sh::kVt);
 
   auto kaddr = [&](int s) { return kd1 + (16 * (s / kMi) + col) * Sh::kKdRow + 2 * (HS / 4) * g + 16 * (s % kMi); };
   auto vaddr = [&](int b) { return vb0 + (16 * b + col) * Sh::kVtRow + 16 * g; };
   bf16x8_t kbuf[kPre], vbuf[kPre];
   float4 ka[2], ke[2], ks[2];
-  float t[NT][2][4], mx[NT], lsum[NT];
+  float t[NT][2][4], lsum[NT];
   u32x4_t pop[NT];
-  bool trig = false;
 
   // softmax of row tile j, item k: 0-1 scores of sub-tile k, 2 the headroom check, 3-6 probabilities of 2 keys
   auto sm_item = [&](int j, int k) {
@@ -452,9 +459,7 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
       const int sub = k;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        float c;
-        if constexpr (KFMT == QP_CODES_INT4) c = fmaf(r.qsum[j], ke[sub][jj], r.m[j]);
-        else c = r.m[j];
+        const float c = fmaf(r.qsum[j], ke[sub][jj], r.m[j]);
         t[j][sub][jj] = fmaf(sprev[j][sub][jj], ka[sub][jj], -c);
       }
       if constexpr (MASK) {
@@ -465,9 +470,21 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
         }
       }
     } else if (k == 2) {
-      mx[j] = fmaxf(fmaxf(fmaxf(t[j][0][0], t[j][0][1]), fmaxf(t[j][0][2], t[j][0][3])),
-                    fmaxf(fmaxf(t[j][1][0], t[j][1][1]), fmaxf(t[j][1][2], t[j][1][3])));
-      trig = trig || __any(mx[j] > kPfRescale);
+      const float mx = fmaxf(fmaxf(fmaxf(t[j][0][0], t[j][0][1]), fmaxf(t[j][0][2], t[j][0][3])),
+                             fmaxf(fmaxf(t[j][1][0], t[j][1][1]), fmaxf(t[j][1][2], t[j][1][3])));
+      if (__builtin_expect(__any(mx > kPfRescale), 0)) {
+        float rm = fmaxf(mx, shfl_xor_f(mx, 16));  // the row's maximum over the tile (row = lane column)
+        rm = fmaxf(rm, shfl_xor_f(rm, 32));
+        const float up = rm > kPfRescale ? rm : 0.f;
+        r.m[j] += up;
+        const float alpha = __builtin_amdgcn_exp2f(-up);
+        r.l[j] *= alpha;
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) t[j][sb][jj] -= up;
+        scale_agpr<17, HS / 16 + 1>(r.acc[j], alpha, rescale_lds);
+      }
       lsum[j] = 0.f;
     } else {
       const int sub = (k - 3) >> 1, h2 = (k - 3) & 1;
@@ -485,7 +502,7 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
 #pragma unroll
   for (int sb = 0; sb < 2; ++sb) {
     ka[sb] = *reinterpret_cast<const float4 *>(kf + 16 * sb + 4 * g);
-    if constexpr (KFMT == QP_CODES_INT4) ke[sb] = *reinterpret_cast<const float4 *>(kf + kPfKeys + 16 * sb + 4 * g);
+    ke[sb] = *reinterpret_cast<const float4 *>(kf + kPfKeys + 16 * sb + 4 * g);
     ks[sb] = *reinterpret_cast<const float4 *>(kf + 2 * kPfKeys + 16 * sb + 4 * g);
   }
 #pragma unroll
@@ -494,8 +511,9 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
     const bf16x8_t kop = kbuf[s % kPre];
     if (s + kPre < kQ) kbuf[s % kPre] = *reinterpret_cast<const bf16x8_t *>(kaddr(s + kPre));
     qk_step<HS, NT>(snew, sub, mi, kop, r.qop);
+    // each K unit's store follows its load by kLag steps, so at most kLag + 1 units are held (int8 keys have 8)
     if (s < St::kNK) st.k_load(s);
-    if (s >= St::kNK && s < 2 * St::kNK) st.k_store(s - St::kNK);
+    if (s >= kLag && s < St::kNK + kLag) st.k_store(s - kLag);
 #pragma unroll
     for (int q = 0; q < NT * kSm; ++q) {
       const int at = 1 + q * (kQ - 1) / (NT * kSm);
@@ -523,18 +541,6 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       if (at(b, c + 8)) st.v_store(c);
-  }
-
-  if (__builtin_expect(trig && may_restart, 0)) {
-    // some score is far above the running maximum: raise it (scores = t + m) and ask for a restart of the pass
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      float rm = mx[j];
-      rm = fmaxf(rm, shfl_xor_f(rm, 16));
-      rm = fmaxf(rm, shfl_xor_f(rm, 32));
-      if (rm > 0.f) r.m[j] += rm;
-    }
-    *restart = it;
   }
 }
 
@@ -627,13 +633,13 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
     const uint16_t *qr = p.q + (int64_t)(q0 + (rv ? tok : 0)) * p.qs0 + (int64_t)(h * G + (rv ? jh : 0)) * p.qs1;
     uint32_t qw[HS / 8];  // channels (HS / 4) g .. + HS / 4 of the row, two per dword (rotated when asked)
     load_query_row<HS / 4>(qw, qr, rv, p.qsigns, g);
-    float qs = 0.f;
+    float qs = 0.f;  // the row's query sum: the 128 offset of the key operands (and the int4 zero point) folds into it
 #pragma unroll
     for (int mi = 0; mi < HS / 32; ++mi) {
       const u32x4_t x = u32x4_t{qw[4 * mi], qw[4 * mi + 1], qw[4 * mi + 2], qw[4 * mi + 3]};
+      qs += bf16_lo(x[0]) + bf16_hi(x[0]) + bf16_lo(x[1]) + bf16_hi(x[1]) + bf16_lo(x[2]) + bf16_hi(x[2]) +
+            bf16_lo(x[3]) + bf16_hi(x[3]);
       if constexpr (KFMT == QP_CODES_INT4) {
-        qs += bf16_lo(x[0]) + bf16_hi(x[0]) + bf16_lo(x[1]) + bf16_hi(x[1]) + bf16_lo(x[2]) + bf16_hi(x[2]) +
-              bf16_lo(x[3]) + bf16_hi(x[3]);
         u32x4_t y;
         y[0] = (x[0] & 0xFFFFu) | (x[2] << 16);
         y[1] = (x[0] >> 16) | (x[2] & 0xFFFF0000u);
@@ -644,10 +650,8 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
         r.qop[jt][mi] = as_bf16x8(x);
       }
     }
-    if constexpr (KFMT == QP_CODES_INT4) {
-      qs += shfl_xor_f(qs, 16);
-      qs += shfl_xor_f(qs, 32);
-    }
+    qs += shfl_xor_f(qs, 16);
+    qs += shfl_xor_f(qs, 32);
     r.qsum[jt] = qs;
     r.m[jt] = -INFINITY;
   }
@@ -665,26 +669,20 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
     if constexpr (SPAN) pf_issue<Sh>(p, trow, tile_key(t), ke, h, w, lane, pk_of(t));
     else pf_gather<Sh>(p, trow, tile_key(t), ke, h, pk_of(t));
   };
-  __shared__ int restart;
-  constexpr int kNoRestart = 0x7fffffff;
   // rows HS + 1 .. HS + 15 of every V^T tile (the zero-point tile's unused rows) stay zero
   constexpr int kZeroDw = 15 * (Sh::kVtRow / 4);
   for (int i = tid; i < 3 * kZeroDw; i += kPfWaves * 64)
     reinterpret_cast<uint32_t *>(smem + Sh::kOffV + (i / kZeroDw) * Sh::kVb + (HS + 1) * Sh::kVtRow)[i % kZeroDw] = 0u;
-  if (tid == 0) restart = kNoRestart;
 
-  // A pass runs over the split's keys with the running maximum m; if a score exceeds m by the headroom, m is raised and
-  // the pass starts over (acc and l restart from zero; m keeps its value). Realistic inputs take one pass; each restart
-  // needs scores 2^64 above the last maximum, and after kPfMaxPasses the pass runs to the end whatever it sees (only
-  // non-finite or adversarial scales get there).
-  for (int pass = 0;; ++pass) {
+  // One pass over the split's keys with the running maximum m of each row, started at the first tile's maximum and
+  // raised in place (l and the accumulators scaled down) when a tile's scores exceed it by more than the headroom.
 #pragma unroll
-    for (int jt = 0; jt < NT; ++jt) {
-      r.l[jt] = 0.f;
+  for (int jt = 0; jt < NT; ++jt) {
+    r.l[jt] = 0.f;
 #pragma unroll
-      for (int b = 0; b <= HS / 16; ++b) r.acc[jt][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    }
-    if (ntiles == 0) break;
+    for (int b = 0; b <= HS / 16; ++b) r.acc[jt][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  if (ntiles > 0) {
     // ---- prologue: tiles 0..2 fetched, 0 and 1 unpacked, tile 3 fetched, S(0) and the initial maximum
     fetch(0);
     if (ntiles > 1) fetch(1);
@@ -722,18 +720,22 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
       nb1 = ctab[b1];
     };
     if (SPAN && ntiles > 4) table_ahead(4);
+    // A rescale parks each accumulator tile in 16 bytes of its lane inside the padding at the end of the V^T rows of
+    // the first V buffer: no copy, stager store or MFMA operand read touches those bytes, so no wave can collide there.
+    static_assert(Sh::kVtRow - kPfKeys * 2 >= 32 && 128 <= Sh::kVtRows, "two 16-byte pad slots per V^T row");
+    const int slot = w * 64 + lane;
+    f32x4_t *rescale_slot =
+        reinterpret_cast<f32x4_t *>(smem + Sh::kOffV + (slot >> 1) * Sh::kVtRow + kPfKeys * 2 + 16 * (slot & 1));
 
-    // One pipeline iteration; false when a restart was requested. Tiles whose keys are all visible to every row come
-    // first and run without the causal mask; the rest (the chunk's own keys) run with it.
-    bool again = false;
-    auto iteration = [&](int it, auto mask_tag) -> bool {
+    // One pipeline iteration. Tiles whose keys are all visible to every row come first and run without the causal
+    // mask; the rest (the chunk's own keys) run with it.
+    auto iteration = [&](int it, auto mask_tag) {
       constexpr bool kMask = decltype(mask_tag)::value;
       if constexpr (SPAN) {
         if (it + 3 < ntiles) wait_vmcnt<Sh::kDmaPerWave>();
         else wait_vmcnt<0>();
       }
       __syncthreads();  // tile it + 1 unpacked by all; tile it + 2 landed; tile it's K and it - 1's V buffers free
-      if (restart < it) return false;  // a wave asked during an earlier tile (every such write precedes the barrier)
       if (it + 4 < ntiles) {  // into slot (it + 1) % 3, unpacked before this barrier
         if constexpr (SPAN) {
           pf_issue_ids<Sh>(p, tile_key(it + 4), ke, nb0, nb1, h, w, lane, pk_of(it + 4));
@@ -751,34 +753,19 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
       st.kend = ke;
       st.tid = tid;
       st.scale_log2 = p.scale_log2;
-      pf_iter<HS, KFMT, NT, kMask>(r, sprev, snew, kd_of(it + 1), vb_of(it), tile_key(it), ke, &restart, it,
-                                   pass + 1 < kPfMaxPasses, st, col, g);
+      pf_iter<HS, KFMT, NT, kMask>(r, sprev, snew, kd_of(it + 1), vb_of(it), tile_key(it), ke, rescale_slot, st, col,
+                                   g);
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         sprev[j][0] = snew[j][0];
         sprev[j][1] = snew[j][1];
       }
-      return true;
     };
     const int nplain = min(ntiles, max(0, (vis_all - kb) / kPfKeys));  // tiles with every key visible to every row
     int it = 0;
-    for (; it < nplain; ++it)
-      if (!iteration(it, std::false_type{})) {
-        again = true;
-        break;
-      }
-    if (!again)
-      for (; it < ntiles; ++it)
-        if (!iteration(it, std::true_type{})) {
-          again = true;
-          break;
-        }
+    for (; it < nplain; ++it) iteration(it, std::false_type{});
+    for (; it < ntiles; ++it) iteration(it, std::true_type{});
     if constexpr (SPAN) wait_vmcnt<0>();
-    __syncthreads();  // no request is written after this point of the pass
-    again = again || restart != kNoRestart;
-    __syncthreads();  // every wave has read the request
-    if (tid == 0) restart = kNoRestart;
-    if (!again) break;
   }
 
   // ---- epilogue: l over the 4 lane groups, zero-point sum from the extra tile, store

@@ -7,6 +7,7 @@ Workloads (24 query / 4 KV heads, head 256, block 16 unless stated):
   prefill-int4-128k-c1024  131072 cached tokens + a 1024-token chunk whose bf16 K/V are quantised by the store
   decode-k8v4-ragged-b32   32 requests of 1 or 2 query tokens, contexts lognormal(ln 16384, 1) clipped to
                            [2048, 65536], int8 keys, queries rotated into the Hadamard domain
+  prefill-k8v4-128k-c1024  the prefill chunk workload over a k8v4 cache (int8 keys stored by the store as well)
 
 int4 cells: nibbles uniform 0..15; per (token, KV head) fp32 scale ~ lognormal(-3, 0.5) with its low 4 mantissa bits
 replaced by the zero point round(U(6, 9)). k8v4 keys: int8 uniform -127..127, fp32 scale ~ lognormal(-4, 0.5).
@@ -21,7 +22,7 @@ import numpy as np
 NQ, NKV, HS, BS = 24, 4, 256, 16
 
 WORKLOADS = ("decode-int4-4k-t1", "decode-int4-128k-t2", "decode-int4-256k-t4", "prefill-int4-128k-c1024",
-             "decode-k8v4-ragged-b32")
+             "decode-k8v4-ragged-b32", "prefill-k8v4-128k-c1024")
 
 
 @dataclass
@@ -120,19 +121,21 @@ def make(name: str, *, small: bool = False) -> Workload:
         return _single(name, rng, 131072 // div, 2)
     if name == "decode-int4-256k-t4":
         return _single(name, rng, 262144 // div, 4)
-    if name == "prefill-int4-128k-c1024":
+    if name in ("prefill-int4-128k-c1024", "prefill-k8v4-128k-c1024"):
+        k8v4 = name.startswith("prefill-k8v4")
         cached, chunk = 131072 // div, 1024 // (4 if small else 1)
         n = cached + chunk
         nb = -(-n // BS)
-        kv = fill_int4_cache(rng, nb)
+        kv = fill_k8v4_cache(rng, nb) if k8v4 else fill_int4_cache(rng, nb)
         table = rng.permutation(nb).astype(np.int32)
         q = bf16_bits(rng.standard_normal((chunk, NQ, HS)).astype(np.float32))
         nk = bf16_bits(rng.standard_normal((chunk, NKV, HS)).astype(np.float32))
         nv = bf16_bits(rng.standard_normal((chunk, NKV, HS)).astype(np.float32))
         pos = np.arange(cached, n)
         slots = (table[pos // BS].astype(np.int64) * BS + pos % BS)
-        return Workload(name, kv, "int4", q, np.array([0, chunk], np.int32), np.array([n], np.int32), table[None, :],
-                        1.0 / 16, new_key=nk, new_value=nv, new_slots=slots, meta={"cached": cached})
+        return Workload(name, kv, "int8" if k8v4 else "int4", q, np.array([0, chunk], np.int32),
+                        np.array([n], np.int32), table[None, :], 1.0 / 16, new_key=nk, new_value=nv, new_slots=slots,
+                        meta={"cached": cached})
     if name == "decode-k8v4-ragged-b32":
         seqs = 32
         T = rng.integers(1, 3, size=seqs)
