@@ -1234,7 +1234,13 @@ int dispatch_hs(const qp_paged_cache *cache, const DecodeParams &p, int nct, dim
 
 template <int HS>
 int dispatch_decode(const DecodeParams &p, int kfmt, int nct, dim3 grid, bool span, hipStream_t s) {
-  if (kfmt == QP_CODES_INT4) {
+  if constexpr (HS == 512) {
+    // Two row tiles at head 512 would need more registers than a wave has (the accumulators alone fill the AGPRs and
+    // the rest spills): every caller runs head 512 as workgroups of at most 16 query rows, so only one tile exists.
+    QP_REQUIRE(nct == 1, "qp_decode_splitkv: head 512 runs one row tile per workgroup");
+    if (kfmt == QP_CODES_INT4) launch_decode<HS, QP_CODES_INT4, 1>(p, grid, span, s);
+    else launch_decode<HS, QP_CODES_INT8, 1>(p, grid, span, s);
+  } else if (kfmt == QP_CODES_INT4) {
     if (nct == 1) launch_decode<HS, QP_CODES_INT4, 1>(p, grid, span, s);
     else launch_decode<HS, QP_CODES_INT4, 2>(p, grid, span, s);
   } else {
