@@ -983,6 +983,70 @@ struct MergeParams {
   const int32_t *skip_seq;
 };
 
+// The token and sequence of merge row srow (wave-uniform): false when the row is served elsewhere.
+__device__ __forceinline__ bool merge_row_owner(const MergeParams &p, int srow, int &tok, int &seq) {
+  if (p.row_tok) {
+    tok = p.row_tok[srow];
+    seq = p.row_seq[srow];
+    return tok >= 0;
+  }
+  tok = srow;
+  int lo = 0, hi = p.num_seqs - 1;
+  while (lo < hi) {  // last sequence whose first query token is <= tok
+    const int mid = (lo + hi + 1) >> 1;
+    if (p.cu_q[mid] <= tok) lo = mid;
+    else hi = mid - 1;
+  }
+  seq = lo;
+  return !(p.skip_seq && p.skip_seq[lo] >= 0);
+}
+
+template <int CPL>
+__device__ __forceinline__ void load_channels(const float *src, float (&v)[CPL]) {
+  if constexpr (CPL >= 4) {
+#pragma unroll
+    for (int i = 0; i < CPL / 4; ++i) {
+      const float4 x = reinterpret_cast<const float4 *>(src)[i];
+      v[4 * i] = x.x;
+      v[4 * i + 1] = x.y;
+      v[4 * i + 2] = x.z;
+      v[4 * i + 3] = x.w;
+    }
+  } else if constexpr (CPL == 2) {
+    const float2 x = *reinterpret_cast<const float2 *>(src);
+    v[0] = x.x;
+    v[1] = x.y;
+  } else {
+    v[0] = *src;
+  }
+}
+
+// Fast Walsh-Hadamard transform of a row of LANES * CPL channels held CPL per lane (lane l: channels CPL l ..), in
+// the butterfly order of an in-LDS transform (span 1, 2, 4, ...; lower + upper, lower - upper), so both give the same
+// bits: spans below CPL inside each lane, the rest as exchanges with lane l ^ (span / CPL) among lanes 0 .. LANES-1.
+template <int CPL, int LANES = 64>
+__device__ __forceinline__ void fwht_lanes(float (&x)[CPL], int lane) {
+#pragma unroll
+  for (int span = 1; span < CPL; span <<= 1) {
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      if (i & span) continue;
+      const float u = x[i], v = x[i | span];
+      x[i] = u + v;
+      x[i | span] = u - v;
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < LANES; o <<= 1) {
+    const bool upper = (lane & o) != 0;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const float other = shfl_xor_f(x[i], o);
+      x[i] = upper ? other - x[i] : x[i] + other;
+    }
+  }
+}
+
 // One workgroup of 256 threads per (token, query head). Thread t owns channels 4 (t % (HS/4)) .. +3 of the segments
 // s = t / (HS/4) + k * (256 / (HS/4)) and folds them in with an online log-sum-exp of its own (a running maximum, the
 // accumulator rescaled when it rises), batch by batch: a batch's segment statistics and rows are all requested before
@@ -1020,10 +1084,16 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
   const int quads = width / 4;
   const int groups = 256 / quads;
   const int cq = t % quads, sg = t / quads;
-  float sgn[4];  // rotation signs of the channels this thread writes, requested with the segment loads
+  // rotation signs of the channels this thread writes, requested with the segment loads: channels 4t .. 4t + 3 when
+  // the rotation runs in registers (head size up to 256), else t, t + 256, ...
+  const bool reg_rht = RHT && p.head_size <= 256;
+  float sgn[4];
   if constexpr (RHT) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) sgn[k] = t + 256 * k < p.head_size ? p.signs[t + 256 * k] * p.out_scale : 0.f;
+    for (int k = 0; k < 4; ++k) {
+      const int c = reg_rht ? 4 * t + k : t + 256 * k;
+      sgn[k] = (reg_rht ? t < quads : c < p.head_size) ? p.signs[c] * p.out_scale : 0.f;
+    }
   }
   float mt = -INFINITY, lt = 0.f;
   float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1089,6 +1159,46 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
   pm[t] = mt;
   pl[t] = lt;
   __syncthreads();
+  if (RHT && reg_rht) {
+    // the 64 or fewer quads of the row are the first lanes of wave 0: combine, rotate in registers, store
+    if (t < quads) {
+      const int count = 256 / 64;
+      float M = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < count; ++k) M = fmaxf(M, pm[t + k * 64]);
+      float x[4] = {0.f, 0.f, 0.f, 0.f};
+      float L = 0.f;
+#pragma unroll
+      for (int k = 0; k < count; ++k) {
+        const float mk = pm[t + k * 64];
+        const float f = mk == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mk - M);
+        const float4 o = part[t + k * 64];
+        x[0] = fmaf(o.x, f, x[0]);
+        x[1] = fmaf(o.y, f, x[1]);
+        x[2] = fmaf(o.z, f, x[2]);
+        x[3] = fmaf(o.w, f, x[3]);
+        L = fmaf(pl[t + k * 64], f, L);
+      }
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) x[k] *= inv;
+      switch (quads) {
+        case 64: fwht_lanes<4, 64>(x, t); break;
+        case 32: fwht_lanes<4, 32>(x, t); break;
+        case 16: fwht_lanes<4, 16>(x, t); break;
+        case 8: fwht_lanes<4, 8>(x, t); break;
+        case 4: fwht_lanes<4, 4>(x, t); break;
+        default: break;
+      }
+      uint16_t *dst = p.out + (int64_t)tok * p.os0 + (int64_t)head * p.os1 + 4 * t;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) dst[k] = f32_to_bf16_bits(x[k] * sgn[k]);
+      if (p.lse && t == 0)
+        p.lse[(int64_t)tok * p.ls0 + (int64_t)head * p.ls1] =
+            (M == -INFINITY || L <= 0.f) ? -INFINITY : (M + __log2f(L)) * 0.6931471805599453f;
+    }
+    return;
+  }
   if (t < quads) {
     const int stride = quads > 64 ? quads : 64, count = 256 / stride;  // distinct states of the quad
     float M = -INFINITY;
@@ -1145,6 +1255,100 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeParams p) {
     p.lse[(int64_t)tok * p.ls0 + (int64_t)head * p.ls1] =
         (M == -INFINITY || L <= 0.f) ? -INFINITY : (M + __log2f(L)) * 0.6931471805599453f;
   }
+}
+
+// One wave per (row, query head), four rows per workgroup, for merges of few segments (the key splits of a prefill
+// chunk, decode batches of many sequences at 16 segments or fewer): every lane folds every segment of its channels
+// CPL l .. CPL l + CPL - 1 (head size 64 CPL), so no state is exchanged between lanes or waves. The row's statistics
+// are wave-uniform. Segments go in batches whose loads are all issued before any is used, past-context segments
+// loaded and ignored (as in merge_kernel). With signs the merged row is rotated back in registers (fwht_lanes).
+template <bool RHT, int CPL>
+__global__ __launch_bounds__(256) void merge_wave_kernel(const MergeParams p, int rows) {
+  const int lane = threadIdx.x & 63;
+  const int srow = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
+  const int head = blockIdx.y;
+  if (srow >= rows) return;
+  int tok, seq;
+  if (!merge_row_owner(p, srow, tok, seq)) return;
+  const int n = p.used_k[seq];
+  const int seg = (n + p.num_segments * QP_DECODE_TILE - 1) / (p.num_segments * QP_DECODE_TILE) * QP_DECODE_TILE;
+  const int active = seg > 0 ? min(p.num_segments, (n + seg - 1) / seg) : 0;
+  const float *mrow = p.smax + (int64_t)srow * p.sts0 + (int64_t)head * p.sts1;
+  const float *lrow = p.ssum + (int64_t)srow * p.sts0 + (int64_t)head * p.sts1;
+  const float *orow = p.so + (int64_t)srow * p.sos0 + (int64_t)head * p.sos1 + CPL * lane;
+  float sgn[CPL];
+  if constexpr (RHT) {
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) sgn[i] = p.signs[CPL * lane + i] * p.out_scale;
+  }
+  constexpr int kBatch = CPL >= 4 ? 64 / CPL : 16;  // at most 64 partial floats in flight per lane
+  float mt = -INFINITY, lt = 0.f;
+  float a[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) a[i] = 0.f;
+  for (int s0 = 0; s0 < p.num_segments; s0 += kBatch) {
+    float v[kBatch][CPL];
+    float ms[kBatch], ls[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int s = s0 + k;
+      if (s < p.num_segments) {
+        load_channels<CPL>(orow + (int64_t)s * p.sos2, v[k]);
+        ms[k] = mrow[s];
+        ls[k] = lrow[s];
+      } else {
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) v[k][i] = 0.f;
+        ms[k] = -INFINITY;
+        ls[k] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k)
+      if (s0 + k >= active) ms[k] = -INFINITY;
+    float bm = mt;
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) bm = fmaxf(bm, ms[k]);
+    if (bm == -INFINITY) continue;
+    const float f = mt == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mt - bm);
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) a[i] *= f;
+    lt *= f;
+    mt = bm;
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      if (ms[k] == -INFINITY) continue;  // an empty segment: its row was not written
+      const float wgt = __builtin_amdgcn_exp2f(ms[k] - mt);
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) a[i] = fmaf(v[k][i], wgt, a[i]);
+      lt = fmaf(ls[k], wgt, lt);
+    }
+  }
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) a[i] *= inv;
+  if constexpr (RHT) {
+    fwht_lanes<CPL>(a, lane);
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) a[i] *= sgn[i];
+  }
+  uint16_t *dst = p.out + (int64_t)tok * p.os0 + (int64_t)head * p.os1 + CPL * lane;
+  if constexpr (CPL >= 2) {
+    if ((reinterpret_cast<uintptr_t>(p.out + (int64_t)tok * p.os0 + (int64_t)head * p.os1) & 3) == 0) {
+#pragma unroll
+      for (int i = 0; i < CPL; i += 2)
+        reinterpret_cast<uint32_t *>(dst)[i / 2] =
+            (uint32_t)f32_to_bf16_bits(a[i]) | ((uint32_t)f32_to_bf16_bits(a[i + 1]) << 16);
+    } else {
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) dst[i] = f32_to_bf16_bits(a[i]);
+    }
+  } else {
+    dst[0] = f32_to_bf16_bits(a[0]);
+  }
+  if (p.lse && lane == 0)
+    p.lse[(int64_t)tok * p.ls0 + (int64_t)head * p.ls1] =
+        (mt == -INFINITY || lt <= 0.f) ? -INFINITY : (mt + __log2f(lt)) * 0.6931471805599453f;
 }
 
 // Query slices of every sequence for the slice prefill: tokens [t0, t0 + ts) of sequence i (the last one shorter),
@@ -1369,9 +1573,32 @@ int check_merge(const qp_merge_args *a) {
   return QP_OK;
 }
 
-// rows workgroups (one per row: token, or segment-buffer row when routed) per query head.
+constexpr int kWaveMergeSegments = 16;  // merges of at most this many segments run one wave per row
+
+template <int CPL>
+void launch_merge_wave(const MergeParams &p, dim3 grid, int rows, hipStream_t s) {
+  if (p.signs) merge_wave_kernel<true, CPL><<<grid, 256, 0, s>>>(p, rows);
+  else merge_wave_kernel<false, CPL><<<grid, 256, 0, s>>>(p, rows);
+}
+
+// Per query head: one wave per row (token, or segment-buffer row when routed) for few segments, else one workgroup
+// per row.
 int launch_merge(const MergeParams &p, int64_t rows, int num_q_heads, hipStream_t s) {
   if (rows <= 0) return QP_OK;
+  const bool pow2 = (p.head_size & (p.head_size - 1)) == 0;
+  if (p.num_segments <= kWaveMergeSegments && p.head_size >= 64 && pow2 && rows <= INT32_MAX) {
+    // few segments: one wave per row (a workgroup per row would leave most of its threads idle)
+    const dim3 grid((unsigned)((rows + 3) / 4), num_q_heads);
+    const int r = (int)rows;
+    switch (p.head_size) {
+      case 64: launch_merge_wave<1>(p, grid, r, s); break;
+      case 128: launch_merge_wave<2>(p, grid, r, s); break;
+      case 256: launch_merge_wave<4>(p, grid, r, s); break;
+      case 512: launch_merge_wave<8>(p, grid, r, s); break;
+      default: launch_merge_wave<16>(p, grid, r, s); break;
+    }
+    return launch_status();
+  }
   // a few rows need the channel split to spread the partial reads over more CUs; many rows fill the device alone
   const int parts = (p.signs || rows * num_q_heads >= 1024 || p.head_size < 64) ? 1 : 4;
   const dim3 grid((unsigned)rows, num_q_heads, parts);
