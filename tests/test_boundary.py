@@ -40,6 +40,71 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert _hip.lib().qp_version().decode().startswith("quantpack-hip")
 
 
+STRUCTS = {"CacheHalf": "qp_cache_half", "PagedCache": "qp_paged_cache", "DecodeArgs": "qp_decode_args",
+           "MergeArgs": "qp_merge_args", "PrefillArgs": "qp_prefill_args", "AttentionArgs": "qp_attention_args",
+           "StoreArgs": "qp_store_args"}
+
+
+def test_ctypes_structs_have_the_header_layout(tmp_path):
+    """Every ctypes Structure of the binding has the size and field offsets that gcc gives the header's struct."""
+    import shutil
+    import subprocess
+
+    from vllm_quantpack import _hip
+    if shutil.which("gcc") is None:
+        pytest.skip("no gcc")
+    lines = ['#include <stddef.h>', '#include <stdio.h>', '#include "quantpack.h"', "int main(void) {"]
+    for py, c in STRUCTS.items():
+        lines.append(f'  printf("{py} size %zu\\n", sizeof({c}));')
+        for name, _ in getattr(_hip, py)._fields_:
+            lines.append(f'  printf("{py} {name} %zu\\n", offsetof({c}, {name}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(REPO, "include"), str(src), "-o", str(exe)], check=True)
+    got = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    want = []
+    for py in STRUCTS:
+        T = getattr(_hip, py)
+        want.append(f"{py} size {ctypes.sizeof(T)}")
+        want += [f"{py} {name} {getattr(T, name).offset}" for name, _ in T._fields_]
+    assert got[:-1] == want
+
+
+@pytest.mark.parametrize("name", list(STRUCTS))
+def test_packer_writes_what_ctypes_writes(name):
+    """Packer (one struct.pack_into) fills a Structure with the same bytes as setting its fields through ctypes."""
+    import random
+
+    from vllm_quantpack import _hip
+    T = getattr(_hip, name)
+    rnd = random.Random(len(name))
+    codes = [c for _, c in _hip._scalars(T)]
+    vals = [rnd.getrandbits(63) if c == "Q" else rnd.randrange(-2**62, 2**62) if c == "q"
+            else rnd.randrange(-2**31, 2**31) if c == "i" else rnd.choice([0.5, -3.25, 1e-3, 7.0]) for c in codes]
+    packed = T()
+    _hip.Packer(T).pack(packed, *vals)
+
+    def fill(obj, it):
+        for field, ftype in type(obj)._fields_:
+            if issubclass(ftype, ctypes.Structure):
+                fill(getattr(obj, field), it)
+            elif issubclass(ftype, ctypes.Array):
+                arr = getattr(obj, field)
+                for i in range(len(arr)):
+                    arr[i] = next(it)
+            else:
+                setattr(obj, field, next(it))
+
+    ref = T()
+    ctypes.memset(ctypes.byref(ref), 0xAB, ctypes.sizeof(T))   # padding differs; fields must not
+    fill(ref, iter(vals))
+    for off, code in _hip._scalars(T):
+        size = ctypes.sizeof({"Q": ctypes.c_void_p, "q": ctypes.c_int64, "i": ctypes.c_int32, "f": ctypes.c_float}[code])
+        assert bytes(packed)[off:off + size] == bytes(ref)[off:off + size], (name, off)
+
+
 def test_argument_errors_are_reported_without_a_gpu():
     """Validation runs on the host before any launch: a bad call returns QP_ERR_INVALID with a message."""
     from vllm_quantpack import _hip

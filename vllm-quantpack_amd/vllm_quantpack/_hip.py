@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import struct
 from ctypes import POINTER, Structure, c_char_p, c_float, c_int32, c_int64, c_void_p
 
 import torch  # noqa: F401  (must be loaded first: see module docstring)
@@ -78,6 +79,50 @@ class StoreArgs(Structure):
                 ("slot_mapping", c_void_p), ("num_tokens", c_int32), ("rht_signs", c_void_p)]
 
 
+_CODES = {c_void_p: "Q", c_int64: "q", c_int32: "i", c_float: "f"}
+
+
+def _scalars(struct_type, base=0):
+    """(byte offset, struct code) of every scalar of a ctypes Structure, nested structures and arrays flattened, in
+    field order."""
+    out = []
+    for name, t in struct_type._fields_:
+        off = base + getattr(struct_type, name).offset
+        if issubclass(t, Structure):
+            out += _scalars(t, off)
+        elif issubclass(t, ctypes.Array):
+            out += [(off + i * ctypes.sizeof(t._type_), _CODES[t._type_]) for i in range(t._length_)]
+        else:
+            out.append((off, _CODES[t]))
+    return out
+
+
+class Packer:
+    """Fills every field of a ctypes Structure in one `struct.pack_into` (about 0.1 us, against about 1 us per
+    nested structure and field for ctypes' own constructor): values in field order, nested structures and arrays
+    flattened, 0 for a null pointer. The format is derived from the Structure's own field offsets, so it has the
+    C layout ctypes computed."""
+
+    def __init__(self, struct_type):
+        fmt, pos = "<", 0
+        for off, code in _scalars(struct_type):
+            if off > pos:
+                fmt += f"{off - pos}x"
+            fmt += code
+            pos = off + struct.calcsize(code)
+        size = ctypes.sizeof(struct_type)
+        if size > pos:
+            fmt += f"{size - pos}x"
+        self._s = struct.Struct(fmt)
+        if self._s.size != size:
+            raise AssertionError(f"{struct_type.__name__}: packed size {self._s.size} != {size}")
+        self.type = struct_type
+        self.fields = len(_scalars(struct_type))
+
+    def pack(self, dst, *values) -> None:
+        self._s.pack_into(dst, 0, *values)
+
+
 # Every entry point of include/quantpack.h with its ctypes signature.
 SIGNATURES = {
     "qp_unpack_segment": (c_int32, [POINTER(CacheHalf), c_int32, c_int32, c_int32, c_void_p, c_int32, c_int32,
@@ -130,7 +175,13 @@ def check(status: int, what: str) -> None:
     raise RuntimeError(f"{what}: HIP error {status}: {msg}")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor):
+    """The current HIP stream of t's device (torch's raw-stream query when it has one: no Stream object)."""
+    if _raw_stream is not None and t.is_cuda:
+        return c_void_p(_raw_stream(t.get_device()))
     return c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
@@ -149,8 +200,29 @@ def cache_half(codes: torch.Tensor, words: torch.Tensor) -> CacheHalf:
                      fmt)
 
 
-def paged_cache(k_cache, v_cache, k_scale_cache, v_scale_cache, head_size: int) -> PagedCache:
+_WORD_DTYPES = (torch.float32, torch.int32, torch.uint32)
+_PAGED = None
+
+
+def pack_paged_cache(dst: PagedCache, k_cache, v_cache, k_scale_cache, v_scale_cache, head_size: int) -> PagedCache:
+    """Fill dst with the cache views' pointers, strides and sizes (the checks of cache_half / paged_cache)."""
+    global _PAGED
+    if _PAGED is None:
+        _PAGED = Packer(PagedCache)
+    if k_cache.element_size() != 1 or v_cache.element_size() != 1:
+        raise ValueError(f"cache codes must be a byte view, got {k_cache.dtype} / {v_cache.dtype}")
     if v_cache.dtype == torch.int8:
         raise ValueError("value codes must be uint8 nibble pairs")
-    return PagedCache(cache_half(k_cache, k_scale_cache), cache_half(v_cache, v_scale_cache), k_cache.shape[0],
-                      k_cache.shape[1], k_cache.shape[2], head_size)
+    if k_scale_cache.dtype not in _WORD_DTYPES or v_scale_cache.dtype not in _WORD_DTYPES:
+        raise ValueError(f"scale words must be 4-byte elements, got {k_scale_cache.dtype} / {v_scale_cache.dtype}")
+    ks, kws, vs, vws = k_cache.stride(), k_scale_cache.stride(), v_cache.stride(), v_scale_cache.stride()
+    shape = k_cache.shape
+    _PAGED.pack(dst, k_cache.data_ptr(), ks[0], ks[1], ks[2], k_scale_cache.data_ptr(), kws[0], kws[1], kws[2],
+                CODES_INT8 if k_cache.dtype == torch.int8 else CODES_INT4,
+                v_cache.data_ptr(), vs[0], vs[1], vs[2], v_scale_cache.data_ptr(), vws[0], vws[1], vws[2], CODES_INT4,
+                shape[0], shape[1], shape[2], head_size)
+    return dst
+
+
+def paged_cache(k_cache, v_cache, k_scale_cache, v_scale_cache, head_size: int) -> PagedCache:
+    return pack_paged_cache(PagedCache(), k_cache, v_cache, k_scale_cache, v_scale_cache, head_size)

@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import contextlib
 import os
+import threading
 
 import torch
 
@@ -77,19 +78,28 @@ def decode_tiles(sms):
     return (int(tile), int(warps), segments) + tuple(int(m) for m in max_m[:1])
 
 
+_ROW_CAP: dict = {}
+
+
 def decode_row_cap(sms) -> int:
     """The query-row cap of VLLM_QUANTPACK_INT4_DECODE's optional fourth value (DECODE_MAX_M by default), as the
-    library takes it: 16 keeps one row tile per split-KV workgroup, anything from 32 up allows two."""
-    tiles = decode_tiles(sms)
-    rows = tiles[3] if len(tiles) > 3 else DECODE_MAX_M
-    return 16 if rows < 32 else MAX_DECODE_ROWS
+    library takes it: 16 keeps one row tile per split-KV workgroup, anything from 32 up allows two. Parsed once per
+    value of the variable."""
+    key = (os.environ.get("VLLM_QUANTPACK_INT4_DECODE"), sms)
+    cap = _ROW_CAP.get(key)
+    if cap is None:
+        tiles = decode_tiles(sms)
+        rows = tiles[3] if len(tiles) > 3 else DECODE_MAX_M
+        cap = _ROW_CAP[key] = 16 if rows < 32 else MAX_DECODE_ROWS
+    return cap
 
 
 _CUS: dict = {}
 
 
-def _device_cus(device):
-    idx = device.index if device.index is not None else torch.cuda.current_device()
+def _device_cus(t: torch.Tensor) -> int:
+    """Compute units of the GPU that holds t."""
+    idx = t.get_device()
     cus = _CUS.get(idx)
     if cus is None:
         cus = _CUS[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
@@ -118,46 +128,61 @@ def _check_batch(q, cu_seqlens_q, seqused_k, block_table):
             raise ValueError(f"int4 KV attention: {name} must be int32, got {t.dtype}")
 
 
-def _segm_fields(so, sm, ss):
+_ATTENTION = _hip.Packer(_hip.AttentionArgs)
+_NO_SEGMENTS = (0,) * 10
+_TLS = threading.local()
+
+
+def _pack_attention(dst, q, out, *, cu_seqlens_q, seqused_k, block_table, max_seqlen_q, max_seqlen_k, softmax_scale,
+                    num_segments=0, softmax_segm_output=None, softmax_segm_max=None, softmax_segm_expsum=None,
+                    rht_signs=None, rht_out_scale=1.0, max_decode_rows=0):
+    so, sm, ss = softmax_segm_output, softmax_segm_max, softmax_segm_expsum
     if so is None or sm is None or ss is None:
-        return dict(segm_output=None, segm_max=None, segm_expsum=None, segm_rows=0)
-    if sm.stride() != ss.stride() or sm.stride(2) != 1:
-        raise ValueError("segment max / expsum buffers must share strides with contiguous segments")
-    return dict(segm_output=so.data_ptr(), segm_output_stride=_hip.I64x3(*so.stride()[:3]), segm_max=sm.data_ptr(),
-                segm_expsum=ss.data_ptr(), segm_stat_stride=_hip.I64x2(sm.stride(0), sm.stride(1)),
-                segm_rows=so.shape[0])
+        segm = _NO_SEGMENTS
+    else:
+        st = sm.stride()
+        if st != ss.stride() or st[2] != 1:
+            raise ValueError("segment max / expsum buffers must share strides with contiguous segments")
+        sost = so.stride()
+        segm = (so.data_ptr(), sost[0], sost[1], sost[2], sm.data_ptr(), ss.data_ptr(), st[0], st[1], so.shape[0],
+                int(num_segments))
+    qs, ost = q.stride(), out.stride()
+    _ATTENTION.pack(dst, q.data_ptr(), qs[0], qs[1], cu_seqlens_q.data_ptr(), seqused_k.data_ptr(),
+                    block_table.data_ptr(), block_table.stride(0), seqused_k.shape[0], q.shape[0], q.shape[1],
+                    int(max_seqlen_q), int(min(max_seqlen_k, 2**31 - 1)), float(softmax_scale), out.data_ptr(), ost[0],
+                    ost[1], *segm, int(max_decode_rows), 0 if rht_signs is None else rht_signs.data_ptr(),
+                    float(rht_out_scale), 0, 0)
+    return dst
 
 
-def attention_args(q, out, *, cu_seqlens_q, seqused_k, block_table, max_seqlen_q, max_seqlen_k, softmax_scale,
-                   num_segments=0, softmax_segm_output=None, softmax_segm_max=None, softmax_segm_expsum=None,
-                   rht_signs=None, rht_out_scale=1.0, max_decode_rows=0) -> _hip.AttentionArgs:
-    """The qp_attention arguments of one call (no workspace yet). q and out bf16 [T, NQ, hs]."""
-    segm = _segm_fields(softmax_segm_output, softmax_segm_max, softmax_segm_expsum)
-    a = _hip.AttentionArgs(q.data_ptr(), _hip.I64x2(q.stride(0), q.stride(1)), cu_seqlens_q.data_ptr(),
-                           seqused_k.data_ptr(), block_table.data_ptr(), block_table.stride(0), len(seqused_k),
-                           q.shape[0], q.shape[1], int(max_seqlen_q), int(min(max_seqlen_k, 2**31 - 1)),
-                           float(softmax_scale), out.data_ptr(), _hip.I64x2(out.stride(0), out.stride(1)))
-    for k, v in segm.items():
-        setattr(a, k, v)
-    a.num_segments = int(num_segments) if segm["segm_rows"] else 0
-    a.max_decode_rows = int(max_decode_rows)
-    a.rht_signs = _hip.ptr(rht_signs)
-    a.rht_out_scale = float(rht_out_scale)
-    return a
+def attention_args(q, out, **kw) -> _hip.AttentionArgs:
+    """The qp_attention arguments of one call (no workspace yet). q and out bf16 [T, NQ, hs]; keywords: cu_seqlens_q,
+    seqused_k, block_table, max_seqlen_q, max_seqlen_k, softmax_scale, and optionally num_segments with the three
+    segment buffers softmax_segm_output / _max / _expsum, rht_signs with rht_out_scale, max_decode_rows."""
+    return _pack_attention(_hip.AttentionArgs(), q, out, **kw)
+
+
+def _scratch():
+    """This thread's argument structs for attend (the library reads them during the call only)."""
+    s = getattr(_TLS, "structs", None)
+    if s is None:
+        s = _TLS.structs = (_hip.PagedCache(), _hip.AttentionArgs())
+    return s
 
 
 def attend(q, k_cache, v_cache, k_scale_cache, v_scale_cache, out, **kw) -> None:
     """One qp_attention call (see attention_args for the keywords): the library routes the batch between split-KV
     decode and prefill on the device. A workspace is taken from torch's caching allocator only when the batch has
     sequences of more than 4 query tokens (a batch of short sequences needs none)."""
-    hs = q.shape[2]
-    cache = _hip.paged_cache(k_cache, v_cache, k_scale_cache, v_scale_cache, hs)
-    args = attention_args(q, out, **kw)
+    cache, args = _scratch()
+    _hip.pack_paged_cache(cache, k_cache, v_cache, k_scale_cache, v_scale_cache, q.shape[2])
+    _pack_attention(args, q, out, **kw)
     lib = _hip.lib()
     need = lib.qp_attention_workspace_size(cache, args)
-    ws = torch.empty(need, dtype=torch.uint8, device=q.device) if need > 0 else None
-    args.workspace = _hip.ptr(ws)
-    args.workspace_bytes = need
+    if need > 0:
+        ws = torch.empty(need, dtype=torch.uint8, device=q.device)
+        args.workspace = ws.data_ptr()
+        args.workspace_bytes = need
     _hip.check(lib.qp_attention(cache, args, _hip.stream_of(q)), "int4 KV attention")
 
 
@@ -209,16 +234,17 @@ def unified_attention_int4(q, k_cache, v_cache, out, *, cu_seqlens_q, max_seqlen
     hs = q.shape[2]
     target = out if (out.dtype == torch.bfloat16 and out.stride(-1) == 1) else torch.empty(
         q.shape, dtype=torch.bfloat16, device=q.device)
-    segments = 0
+    segments = rows = 0
     if softmax_segm_output is not None and num_par_softmax_segments:
-        cus = _device_cus(q.device)
-        segments = decode_segments(num_par_softmax_segments, len(seqused_k), k_cache.shape[2], cus)
+        cus = _device_cus(q)
+        segments = decode_segments(num_par_softmax_segments, seqused_k.shape[0], k_cache.shape[2], cus)
+        rows = decode_row_cap(cus)
     attend(q, k_cache, v_cache, k_scale_cache, v_scale_cache, target, cu_seqlens_q=cu_seqlens_q,
            seqused_k=seqused_k, block_table=block_table, max_seqlen_q=max_seqlen_q, max_seqlen_k=max_seqlen_k,
            softmax_scale=float(softmax_scale) / hs,        # <R q, R k> = hs <q, k>
            num_segments=segments, softmax_segm_output=softmax_segm_output, softmax_segm_max=softmax_segm_max,
            softmax_segm_expsum=softmax_segm_expsum, rht_signs=rht.signs(hs, q.device), rht_out_scale=1.0 / hs,
-           max_decode_rows=decode_row_cap(_device_cus(q.device)) if segments else 0)
+           max_decode_rows=rows)
     if target is not out:
         out.copy_(target)
     return None
