@@ -219,6 +219,32 @@ __device__ __forceinline__ void rotate_row_quad(float (&x)[E], const float *sign
     }
 }
 
+// Fast Walsh-Hadamard transform of a row of LANES * CPL channels held CPL per lane (lane l: channels CPL l ..), in
+// the butterfly order of an in-LDS transform (span 1, 2, 4, ...; lower + upper, lower - upper), so both give the same
+// bits: spans below CPL inside each lane, the rest as exchanges with lane l ^ (span / CPL) among lanes 0 .. LANES-1.
+template <int CPL, int LANES = 64>
+__device__ __forceinline__ void fwht_lanes(float (&x)[CPL], int lane) {
+#pragma unroll
+  for (int span = 1; span < CPL; span <<= 1) {
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      if (i & span) continue;
+      const float u = x[i], v = x[i | span];
+      x[i] = u + v;
+      x[i | span] = u - v;
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < LANES; o <<= 1) {
+    const bool upper = (lane & o) != 0;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const float other = shfl_xor_f(x[i], o);
+      x[i] = upper ? other - x[i] : x[i] + other;
+    }
+  }
+}
+
 // One query row as bf16 (E channels per lane group, 16-byte aligned rows), rotated first when signs is set. The
 // result (bf16 bits, two channels per dword) is what an unrotated caller would have stored after rounding the rotated
 // row to bf16, as the reference feeds its kernel `single_rht(q).to(q.dtype)` (int4_kv.py:326).

@@ -149,9 +149,42 @@ struct WaveState {
   f32x4_t acc[NCT][kNb * 4];            // O^T tiles: tile (b, c) row j -> channel 64 b + 16 g + 4 j + c
 };
 
+// The workgroup's query rows rotated once, for every wave to read: row r (< T G, the rest zero) by wave r % WAVES with
+// all 64 lanes (HS / 64 channels per lane), x D then H in the channel-bit order of rht_kernel and load_query_row, so
+// the bf16 rows are bit-identical to theirs. Each wave rotating all rows itself (about 900 instructions per lane at
+// head 256, before its first copy could issue) cost 3 us of a 131072-key decode.
+template <int HS, int NCT, int WAVES>
+__device__ __forceinline__ void rotate_rows_shared(uint16_t *qrot, const DecodeParams &p, int q0, int T, int h, int G,
+                                                   int w, int lane) {
+  constexpr int CPL = HS / 64;
+  static_assert(CPL == 2 || CPL == 4 || CPL == 8 || CPL == 16, "head size");
+  const int R = T * G;
+  for (int r = w; r < NCT * 16; r += WAVES) {
+    uint32_t *dst = reinterpret_cast<uint32_t *>(qrot + r * HS + CPL * lane);
+    if (r < R) {
+      const int t = r / G, j = r % G;
+      const uint32_t *src = reinterpret_cast<const uint32_t *>(p.q + (int64_t)(q0 + t) * p.qs0 +
+                                                               (int64_t)(h * G + j) * p.qs1 + CPL * lane);
+      float x[CPL];
+#pragma unroll
+      for (int i = 0; i < CPL / 2; ++i) {
+        const uint32_t v = src[i];
+        x[2 * i] = bf16_lo(v) * p.qsigns[CPL * lane + 2 * i];
+        x[2 * i + 1] = bf16_hi(v) * p.qsigns[CPL * lane + 2 * i + 1];
+      }
+      fwht_lanes<CPL>(x, lane);
+#pragma unroll
+      for (int i = 0; i < CPL / 2; ++i) dst[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < CPL / 2; ++i) dst[i] = 0u;
+    }
+  }
+}
+
 template <int HS, int KFMT, int NCT>
 __device__ __forceinline__ void init_state(WaveState<HS, KFMT, NCT> &st, const DecodeParams &p, int q0, int T, int n,
-                                           int h, int G, int col, int g) {
+                                           int h, int G, int col, int g, const uint16_t *qrot = nullptr) {
   const int R = T * G;
 #pragma unroll
   for (int ct = 0; ct < NCT; ++ct) {
@@ -159,9 +192,13 @@ __device__ __forceinline__ void init_state(WaveState<HS, KFMT, NCT> &st, const D
     const bool rv = r < R;
     const int t = (rv ? r : R - 1) / G, j = (rv ? r : R - 1) % G;
     st.row_pos[ct] = n - T + t;
-    const uint16_t *qr = p.q + (int64_t)(q0 + t) * p.qs0 + (int64_t)(h * G + j) * p.qs1;
     uint32_t qw[HS / 8];  // channels (HS / 4) g .. + HS / 4 of the row, two per dword (rotated when asked)
-    load_query_row<HS / 4>(qw, qr, rv, p.qsigns, g);
+    if (qrot) {
+      load_query_row<HS / 4>(qw, qrot + r * HS, rv, nullptr, g);  // rotated by the workgroup (rotate_rows_shared)
+    } else {
+      const uint16_t *qr = p.q + (int64_t)(q0 + t) * p.qs0 + (int64_t)(h * G + j) * p.qs1;
+      load_query_row<HS / 4>(qw, qr, rv, p.qsigns, g);
+    }
     float qs = 0.f;
 #pragma unroll
     for (int mi = 0; mi < HS / 32; ++mi) {
@@ -871,6 +908,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
   // state then fits the VGPRs without spills. Every wave of the workgroup attends the same rows.
   constexpr bool kQL = NCT == 2 && HS <= 256;
   __shared__ bf16x8_t qsh[kQL ? NCT * (HS / 32) * 64 : 1];
+  // Rotated query rows (rotate_rows_shared): their own buffer at one row tile; with two the stage cells hold them until
+  // every wave has read its operands (one more barrier before the first copies).
+  constexpr bool kQrotOwn = NCT == 1;
+  __shared__ __attribute__((aligned(16))) uint16_t qrot_own[kQrotOwn ? 16 * HS : 8];
+  uint16_t *const qrot = kQrotOwn ? qrot_own : reinterpret_cast<uint16_t *>(smem);
+  static_assert(kQrotOwn || NCT * 16 * HS * 2 <= kLds, "rotated rows in the stage cells");
 
   const int lane = threadIdx.x & 63;
   const int w = uniform(threadIdx.x >> 6);
@@ -886,6 +929,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
   // segment, so all waves of the workgroup finish together.
   __shared__ int next_chunk;
   if (threadIdx.x == 0) next_chunk = kStages * WAVES;
+  const bool shared_rot = p.qsigns != nullptr;
+  if (shared_rot) rotate_rows_shared<HS, NCT, WAVES>(qrot, p, q0, T, h, G, w, lane);
   __syncthreads();
 
   uint8_t *wl = smem + w * kStages * 2 * Sh::kHalf;
@@ -896,13 +941,16 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
 
   // The query rows load first: their wait is on the vm counter, which would otherwise also wait for the copies.
   WaveState<HS, KFMT, NCT> st;
-  init_state(st, p, q0, T, n, h, G, col, g);
+  init_state(st, p, q0, T, n, h, G, col, g, shared_rot ? qrot : nullptr);
   if constexpr (kQL) {
     // every wave stores the same operands, and reads back only what its own lanes stored
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
       for (int mi = 0; mi < HS / 32; ++mi) qsh[(ct * (HS / 32) + mi) * 64 + lane] = st.qop[ct][mi];
+  }
+  if constexpr (!kQrotOwn) {
+    if (shared_rot) __syncthreads();  // every wave has read the rotated rows: the stage cells are free again
   }
   int cid[kStages];  // chunk in each stage (issue order alternates between stages), -1 = empty
 #pragma unroll
@@ -1018,32 +1066,6 @@ __device__ __forceinline__ void load_channels(const float *src, float (&v)[CPL])
     v[1] = x.y;
   } else {
     v[0] = *src;
-  }
-}
-
-// Fast Walsh-Hadamard transform of a row of LANES * CPL channels held CPL per lane (lane l: channels CPL l ..), in
-// the butterfly order of an in-LDS transform (span 1, 2, 4, ...; lower + upper, lower - upper), so both give the same
-// bits: spans below CPL inside each lane, the rest as exchanges with lane l ^ (span / CPL) among lanes 0 .. LANES-1.
-template <int CPL, int LANES = 64>
-__device__ __forceinline__ void fwht_lanes(float (&x)[CPL], int lane) {
-#pragma unroll
-  for (int span = 1; span < CPL; span <<= 1) {
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      if (i & span) continue;
-      const float u = x[i], v = x[i | span];
-      x[i] = u + v;
-      x[i | span] = u - v;
-    }
-  }
-#pragma unroll
-  for (int o = 1; o < LANES; o <<= 1) {
-    const bool upper = (lane & o) != 0;
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const float other = shfl_xor_f(x[i], o);
-      x[i] = upper ? other - x[i] : x[i] + other;
-    }
   }
 }
 
