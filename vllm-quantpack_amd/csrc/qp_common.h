@@ -368,16 +368,18 @@ __device__ __forceinline__ void table_pair(const int32_t *trow, int i0, int i1, 
 // later MFMA reads a tile.
 template <int N, int USED = N>
 __device__ __forceinline__ void scale_agpr(f32x4_t (&acc)[N], float alpha, f32x4_t *rs) {
-  const uint32_t at = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) f32x4_t *)rs;
+  // an LDS-typed pointer: the round trip is ds_read / ds_write on a 32-bit address, not flat accesses
+  volatile __attribute__((address_space(3))) f32x4_t *ls = (volatile __attribute__((address_space(3))) f32x4_t *)rs;
+  const uint32_t at = (uint32_t)(uintptr_t)ls;
 #pragma unroll
   for (int i = 0; i < USED; ++i) {
     asm volatile("ds_write_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" ::"v"(at), "a"(acc[i]) : "memory");
-    f32x4_t t = *reinterpret_cast<volatile f32x4_t *>(rs);
+    f32x4_t t = *ls;
     t[0] *= alpha;
     t[1] *= alpha;
     t[2] *= alpha;
     t[3] *= alpha;
-    *reinterpret_cast<volatile f32x4_t *>(rs) = t;
+    *ls = t;
     asm volatile("s_waitcnt lgkmcnt(0)\n\tds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=a"(acc[i]) : "v"(at) : "memory");
   }
 }
