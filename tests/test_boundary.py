@@ -332,3 +332,34 @@ def test_inline_mfma_wait_scan():
     # a VGPR destination too
     vdst = ";;#ASMSTART\n\tv_mfma_f32_16x16x32_bf16 v[20:23], v[4:7], v[8:11], v[20:23]\n;;#ASMEND\n\tv_mov_b32 v0, v21\n"
     assert len(scan(vdst)) == 1
+
+
+def test_spill_scan_flags_scratch_in_mfma_blocks():
+    """The build fails when spill code shares a basic block with MFMAs (the steady-state loop); spills stored before
+    the loop and reloaded on other blocks pass."""
+    scan = _build_module().spills_in_mfma_blocks
+    mfma = "\tv_mfma_f32_16x16x32_bf16 v[0:3], v[4:7], v[8:11], 0\n"
+    hot = f"kern:\n.LBB0_1:                                ; in Loop\n{mfma}\tscratch_load_dword v5, off, off ; Reload\n"
+    assert scan(hot) == [("kern", ".LBB0_1", "scratch_load_dword v5, off, off")]
+    cold = (f"kern:\n\tscratch_store_dword off, v5, off\n.LBB0_1:\n{mfma}\ts_cbranch_scc1 .LBB0_1\n"
+            ".LBB0_2:\n\tscratch_load_dword v5, off, off\n")
+    assert scan(cold) == []
+    # a new function resets the block state; comment lines are not labels
+    two = f"k1:\n{mfma}; %bb.3:\nk2:\n\tscratch_load_dword v5, off, off\n"
+    assert scan(two) == []
+
+
+def test_built_kernels_keep_spills_off_the_mfma_blocks():
+    """Every kernel source with MFMAs, compiled as the build does, has no spill code in an MFMA block."""
+    import shutil
+    import subprocess
+    build = _build_module()
+    if shutil.which(build.hipcc()) is None and not os.path.exists(build.hipcc()):
+        pytest.skip("no hipcc")
+    asm = os.path.join(build.OBJ, "qp_prefill.gfx.s")
+    if not os.path.exists(asm):
+        pytest.skip("not built")
+    for name in ("qp_decode", "qp_prefill"):
+        text = open(os.path.join(build.OBJ, f"{name}.gfx.s")).read()
+        assert "v_mfma" in text
+        assert build.spills_in_mfma_blocks(text) == [], name

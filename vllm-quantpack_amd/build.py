@@ -109,6 +109,38 @@ def mfma_hazards(asm):
     return found
 
 
+_FUNC = re.compile(r"^[A-Za-z_][\w.$]*:")
+_BLOCK = re.compile(r"^\.LBB\d+_\d+:")
+
+
+def spills_in_mfma_blocks(asm):
+    """[(function, block, instruction)] of scratch accesses in basic blocks that also issue MFMAs. Kernels whose
+    register state spills at all must keep the spill code off the MFMA loop (where it is stored once and reloaded on
+    rare paths), and this check holds them to it."""
+    found = []
+    fn = block = None
+    has_mfma, scratch = False, []
+
+    def close():
+        if has_mfma:
+            found.extend((fn, block, s) for s in scratch)
+
+    for raw in asm.splitlines():
+        l = raw.strip()
+        if _FUNC.match(raw):
+            close()
+            fn, block, has_mfma, scratch = raw.split(":")[0], "entry", False, []
+        elif _BLOCK.match(l):
+            close()
+            block, has_mfma, scratch = l.split(":")[0], False, []
+        elif l.startswith("v_mfma"):
+            has_mfma = True
+        elif l.startswith("scratch_"):
+            scratch.append(l.split(";")[0].strip())
+    close()
+    return found
+
+
 def has_inline_mfma(text):
     """Whether a source holds an inline-assembly MFMA, wherever it stands in its assembly string."""
     return re.search(r'asm\s+volatile\s*\(\s*"[^;]*?v_mfma', text) is not None
@@ -125,10 +157,15 @@ def _check_inline_mfma(src, verbose):
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc -S failed on {src}:\n{r.stdout}\n{r.stderr}")
-    bad = mfma_hazards(open(out).read())
+    asm = open(out).read()
+    bad = mfma_hazards(asm)
     if bad:
         lines = "\n".join(f"  {a}: {b}  ->  {c}" for a, b, c in bad[:10])
         raise RuntimeError(f"{src}: MFMA results read within {MFMA_WAIT} wait states:\n{lines}")
+    spills = spills_in_mfma_blocks(asm)
+    if spills:
+        lines = "\n".join(f"  {f} {b}: {i}" for f, b, i in spills[:10])
+        raise RuntimeError(f"{src}: spill code in MFMA blocks:\n{lines}")
 
 
 def build(jobs=None, verbose=False):
