@@ -73,8 +73,7 @@ struct PfShape {
   static constexpr int kCell = kKeyBytes + 4 + HS / 2 + 4;
   static constexpr int kRunUnits = kCell;  // 16-byte units of one 16-cell page run
   static constexpr int kTileUnits = 2 * kRunUnits;
-  static constexpr int kDmaPerWave = (kTileUnits + kPfWaves * 64 - 1) / (kPfWaves * 64);
-  static constexpr int kPk = kDmaPerWave * kPfWaves * 1024;  // packed slot (the copies' tail lands in padding)
+  static constexpr int kPk = (kTileUnits + kPfWaves * 64 - 1) / (kPfWaves * 64) * kPfWaves * 1024;  // packed slot
   static constexpr int kKdRow = HS * 2 + 16;                 // bf16 K row, padded: conflict-free 16 B reads
   static constexpr int kVtRow = kPfKeys * 2 + 32;            // bf16 V^T row (padding 32 B: 4 % faster than 16 B)
   static constexpr int kVtRows = HS + 16;                    // + the zero-point tile
@@ -89,42 +88,83 @@ struct PfShape {
   static_assert(kLds <= 160 * 1024, "LDS");
 };
 
-// Copies the packed cells of keys [k0, k0 + 32) into slot pk: 16-byte unit u of the tile image (run u / kRunUnits,
-// cells back to back) goes to pk + 16 u. Wave w's copy i covers units 64 (4 i + w) + lane; units past the image
-// re-read unit 0 into the padding. A run at or past kend re-reads run 0, so only valid blocks are addressed.
-// Block-table indices of the two page runs of the tile at key k0 (a run at or past kend repeats run 0).
+// Block-table indices of the two page runs of the tile at key k0 (a run at or past kend repeats run 0, so only valid
+// blocks are addressed).
 __device__ __forceinline__ void pf_runs(const PrefillParams &p, int k0, int kend, int &key1, int &b0, int &b1) {
   key1 = uniform(k0 + 16 < kend ? k0 + 16 : k0);
   b0 = uniform(fast_div(k0, p.bs_magic, p.bs_shift));
   b1 = uniform(fast_div(key1, p.bs_magic, p.bs_shift));
 }
 
-template <class Sh>
-__device__ __forceinline__ void pf_issue_ids(const PrefillParams &p, int k0, int kend, int bid0, int bid1, int h,
-                                             int w, int lane, uint8_t *pk) {
-  int key1, b0, b1;
-  pf_runs(p, k0, kend, key1, b0, b1);
-  const uint8_t *run0 =
-      p.kcodes + (int64_t)bid0 * p.ks0 + (int64_t)h * p.ks2 + (int64_t)(k0 - b0 * p.block_size) * Sh::kCell;
-  const uint8_t *run1 =
-      p.kcodes + (int64_t)bid1 * p.ks0 + (int64_t)h * p.ks2 + (int64_t)(key1 - b1 * p.block_size) * Sh::kCell;
-#pragma unroll
-  for (int i = 0; i < Sh::kDmaPerWave; ++i) {
-    const int chunk = kPfWaves * i + w;
-    const int u = 64 * chunk + lane;
-    const uint8_t *src =
-        u < Sh::kRunUnits ? run0 + 16 * u : (u < Sh::kTileUnits ? run1 + 16 * (u - Sh::kRunUnits) : run0);
-    dma16(src, pk + 1024 * chunk);
-  }
+// One dwordx4 per lane from base + voff straight into LDS at dst + 16 * lane (global_load_lds_dwordx4 with a scalar
+// base: the lane offset is the only vector operand).
+__device__ __forceinline__ void dma16_run(const uint8_t *base, uint32_t voff, uint8_t *dst) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint32_t lds =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)dst);
+  // (readfirstlane returns a signed int: each half is widened as unsigned, or a low word with bit 31 set would
+  // sign-extend over the high word)
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)base);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)((uintptr_t)base >> 32));
+  const uint64_t b = ((uint64_t)hi << 32) | (uint64_t)lo;
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(b), "s"(lds)
+               : "memory", "m0");
+#endif
 }
 
+// HBM -> LDS copies of a tile's two 16-cell page runs into its packed slot (run r's unit u at pk + 16 (r kRunUnits +
+// u)). Each run goes in kChunks copies of 64 units, the last one partial (lanes past the run do not copy), and copy q
+// of the tile's 2 kChunks goes to wave q % 4. A copy reads one run: the run's scalar base plus the lane's fixed
+// offset, so a tile costs the waves two run bases and one M0 per copy, and no per-lane address arithmetic.
 template <class Sh>
-__device__ __forceinline__ void pf_issue(const PrefillParams &p, const int32_t *trow, int k0, int kend, int h, int w,
-                                         int lane, uint8_t *pk) {
-  int key1, b0, b1, bid0, bid1;
+struct PfCopies {
+  static constexpr int kChunks = (Sh::kRunUnits + 63) / 64;
+  static constexpr int kTail = Sh::kRunUnits - 64 * (kChunks - 1);  // lanes of a run's last copy
+  static constexpr int kCopies = 2 * kChunks;
+  static constexpr int kMax = (kCopies + kPfWaves - 1) / kPfWaves;   // copies of the busiest wave per tile
+  int w, lane, n;                                                    // n: this wave's copies per tile
+
+  __device__ __forceinline__ PfCopies(int w_, int lane_)
+      : w(w_), lane(lane_), n((kCopies - w_ + kPfWaves - 1) / kPfWaves) {}
+
+  __device__ __forceinline__ void issue(const uint8_t *base0, const uint8_t *base1, uint8_t *pk) const {
+#pragma unroll
+    for (int i = 0; i < kMax; ++i) {
+      const int q = kPfWaves * i + w;
+      if (i + 1 < kMax || q < kCopies) {  // wave-uniform
+        const int r = q / kChunks, c = q % kChunks;
+        const int u = 64 * c;  // first unit of the copy within its run
+        if (kTail == 64 || c + 1 < kChunks || lane < kTail)
+          dma16_run(r ? base1 : base0, 16 * (u + lane), pk + 16 * (r * Sh::kRunUnits + u));
+      }
+    }
+  }
+  // waits until at most K tiles' copies of this wave are outstanding
+  template <int K>
+  __device__ __forceinline__ void wait() const {
+    if (n == kMax) wait_vmcnt<K * kMax>();
+    else wait_vmcnt<K * (kMax - 1)>();
+  }
+};
+
+// Run bases of the tile at key k0 from its block ids: the KV head's cells start at hbase, blocks are ks0 bytes apart
+// (below 2^31: the host takes this path only then), a run starts at its slot.
+struct PfRunBases {
+  int bid0, bid1, soff0, soff1;  // block ids; byte offsets of the runs' first cells within their blocks
+  __device__ __forceinline__ const uint8_t *base0(const uint8_t *hbase, uint32_t ks0) const {
+    return hbase + (uint64_t)(uint32_t)bid0 * ks0 + soff0;
+  }
+  __device__ __forceinline__ const uint8_t *base1(const uint8_t *hbase, uint32_t ks0) const {
+    return hbase + (uint64_t)(uint32_t)bid1 * ks0 + soff1;
+  }
+};
+
+template <class Sh>
+__device__ __forceinline__ void pf_slots(const PrefillParams &p, int k0, int kend, PfRunBases &rb, int &b0, int &b1) {
+  int key1;
   pf_runs(p, k0, kend, key1, b0, b1);
-  table_pair(trow, b0, b1, bid0, bid1);
-  pf_issue_ids<Sh>(p, k0, kend, bid0, bid1, h, w, lane, pk);
+  rb.soff0 = uniform((k0 - b0 * p.block_size) * Sh::kCell);
+  rb.soff1 = uniform((key1 - b1 * p.block_size) * Sh::kCell);
 }
 
 // Strided fallback: the same packed image gathered dword by dword through VGPRs (any 4-byte aligned views).
@@ -668,9 +708,19 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
   auto kd_of = [&](int t) { return smem + Sh::kOffK + (t & 1) * Sh::kKd; };
   auto vb_of = [&](int t) { return smem + Sh::kOffV + (t % 3) * Sh::kVb; };
   auto tile_key = [&](int t) { return kb + t * kPfKeys; };
+  const PfCopies<Sh> copies(w, lane);
+  const uint8_t *hbase = p.kcodes + (int64_t)h * p.ks2;
+  const uint32_t ks0 = (uint32_t)p.ks0;
   auto fetch = [&](int t) {  // packed image of tile t into its slot
-    if constexpr (SPAN) pf_issue<Sh>(p, trow, tile_key(t), ke, h, w, lane, pk_of(t));
-    else pf_gather<Sh>(p, trow, tile_key(t), ke, h, pk_of(t));
+    if constexpr (SPAN) {
+      PfRunBases rb;
+      int b0, b1;
+      pf_slots<Sh>(p, tile_key(t), ke, rb, b0, b1);
+      table_pair(trow, b0, b1, rb.bid0, rb.bid1);
+      copies.issue(rb.base0(hbase, ks0), rb.base1(hbase, ks0), pk_of(t));
+    } else {
+      pf_gather<Sh>(p, trow, tile_key(t), ke, h, pk_of(t));
+    }
   };
   // rows HS + 1 .. HS + 15 of every V^T tile (the zero-point tile's unused rows) stay zero
   constexpr int kZeroDw = 15 * (Sh::kVtRow / 4);
@@ -691,15 +741,15 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
     if (ntiles > 1) fetch(1);
     if (ntiles > 2) fetch(2);
     if constexpr (SPAN) {
-      if (ntiles > 2) wait_vmcnt<2 * Sh::kDmaPerWave>();
-      else if (ntiles > 1) wait_vmcnt<Sh::kDmaPerWave>();
+      if (ntiles > 2) copies.template wait<2>();
+      else if (ntiles > 1) copies.template wait<1>();
       else wait_vmcnt<0>();
     }
     __syncthreads();
     pf_unpack_k<HS, KFMT>(pk_of(0), kd_of(0), tid);
     pf_unpack_v<HS, KFMT>(pk_of(0), vb_of(0), tile_key(0), ke, p.scale_log2, tid);
     if constexpr (SPAN) {
-      if (ntiles > 2) wait_vmcnt<Sh::kDmaPerWave>();
+      if (ntiles > 2) copies.template wait<1>();
       else wait_vmcnt<0>();
     }
     __syncthreads();  // tile 0 unpacked; slot 0 free; tile 1 landed
@@ -715,12 +765,12 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
     // block ids of tile 4, fetched a tile ahead of its copy through the scalar cache (constant address space: the
     // compiler issues s_load and places the lgkm wait itself, and the vm counter of the copies is left alone)
     const __attribute__((address_space(4))) int32_t *ctab = (const __attribute__((address_space(4))) int32_t *)trow;
-    int nb0 = 0, nb1 = 0;
+    PfRunBases ahead{};
     auto table_ahead = [&](int t) {
-      int key1, b0, b1;
-      pf_runs(p, tile_key(t), ke, key1, b0, b1);
-      nb0 = ctab[b0];
-      nb1 = ctab[b1];
+      int b0, b1;
+      pf_slots<Sh>(p, tile_key(t), ke, ahead, b0, b1);
+      ahead.bid0 = ctab[b0];
+      ahead.bid1 = ctab[b1];
     };
     if (SPAN && ntiles > 4) table_ahead(4);
     // A rescale parks each accumulator tile in 16 bytes of its lane inside the padding at the end of the V^T rows of
@@ -741,13 +791,13 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
       auto kd_at = [&](int k) { return PH >= 0 ? smem + Sh::kOffK + ((PH + k) & 1) * Sh::kKd : kd_of(it + k); };
       auto vb_at = [&](int k) { return PH >= 0 ? smem + Sh::kOffV + ((PH + k) % 3) * Sh::kVb : vb_of(it + k); };
       if constexpr (SPAN) {
-        if (it + 3 < ntiles) wait_vmcnt<Sh::kDmaPerWave>();
+        if (it + 3 < ntiles) copies.template wait<1>();
         else wait_vmcnt<0>();
       }
       __syncthreads();  // tile it + 1 unpacked by all; tile it + 2 landed; tile it's K and it - 1's V buffers free
       if (it + 4 < ntiles) {  // into slot (it + 1) % 3, unpacked before this barrier
         if constexpr (SPAN) {
-          pf_issue_ids<Sh>(p, tile_key(it + 4), ke, nb0, nb1, h, w, lane, pk_at(4));
+          copies.issue(ahead.base0(hbase, ks0), ahead.base1(hbase, ks0), pk_at(4));
           if (it + 5 < ntiles) table_ahead(it + 5);
         } else {
           fetch(it + 4);
@@ -999,7 +1049,7 @@ int prefill_run(const qp_paged_cache *cache, const qp_prefill_args *a, const int
   // sequence s owns query blocks [cu_q[s] / BQ + s, cu_q[s + 1] / BQ + s + 1): an upper bound known on the host
   const unsigned blocks = (unsigned)(a->num_tokens / bq + a->num_seqs);
   const dim3 grid(blocks, cache->num_kv_heads, splits);
-  const bool span = is_span_layout(cache) && !getenv("QP_PREFILL_ROWS");
+  const bool span = is_span_layout(cache) && cache->key.code_stride[0] < (int64_t(1) << 31) && !getenv("QP_PREFILL_ROWS");
   if (hs == 256) {
     if (cache->key.format == QP_CODES_INT4) dispatch_nt<256, QP_CODES_INT4>(p, nt, grid, span, s);
     else dispatch_nt<256, QP_CODES_INT8>(p, nt, grid, span, s);
