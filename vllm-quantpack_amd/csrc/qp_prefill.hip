@@ -12,7 +12,8 @@
 // BQ tokens x the G query heads of the KV head, cut into 4 * NT row tiles of 16 rows; wave w owns tiles w, w + 4,
 // w + 8, so each K / V operand read from LDS feeds NT MFMAs and every K/V tile is dequantised once for all G heads.
 // Per 32-key tile, with one barrier:
-//   * the tile's two 16-key page runs come HBM -> LDS (global_load_lds_dwordx4), up to three tiles ahead;
+//   * the tile's two 16-key page runs come HBM -> LDS (global_load_lds_dwordx4) into one of three packed slots,
+//     issued four tiles ahead of the tile whose PV runs, from one scalar base per page run and fixed lane offsets;
 //   * all threads unpack the next tile to exact bf16 integers: K rows (128 + n, channel order permuted like the
 //     query operand), V^T rows (16 + n, keys in MFMA K-slot order) plus a 17th channel tile whose first row holds
 //     16 + zp_v, so the zero-point sum sum_k P16_k (16 + zp_v,k) comes out of the PV MFMA instead of the VALU. The
@@ -20,11 +21,14 @@
 //     of one split, fp32 rounding of the offset-128 sums alone measured 0.5-0.9 % of the output;
 //   * each wave runs S^T = K Q^T (v_mfma_f32_16x16x32_bf16, K as the A operand), the softmax in registers and
 //     O^T += V^T P^T with P^T straight from the S^T registers.
-// The unpack of tile i + 1 sits in the same basic blocks as the MFMAs of tile i, so the scheduler interleaves them
-// (a 16x16x32 MFMA holds the VALU issue for about half of its 16 cycles; the rest is free for VALU work).
-// The running maximum is raised lazily: a tile rescales only when one of its scores exceeds the maximum by 2^8, so
-// the common path spends 2 VALU ops on a score instead of 3 plus a row reduction. Probabilities are then relative
-// to a maximum that may trail the true one by < 2^8, which leaves acc, l and acc / l consistent.
+// The unpack of tile i + 2 sits in the same basic blocks as the QK MFMAs of tile i + 1 and the PV MFMAs of tile i,
+// so the scheduler interleaves them. With one wave per SIMD only about one VALU instruction per 16-cycle MFMA comes
+// free (measured marginal costs of about 1, 2, 3 and 4.5 cycles for the first to the fourth), so the VALU count per
+// tile sets much of the time.
+// The running maximum is raised lazily: a tile rescales only when one of its scores exceeds the maximum by more than
+// kPfRescale (64 in log2 units), so the common path spends 2 VALU ops on a score instead of 3 plus a row reduction.
+// Probabilities are then relative to a maximum that may trail the true one by up to 2^64, far inside fp32's range,
+// which leaves acc, l and acc / l consistent.
 // When the query blocks alone cannot fill the CUs, keys are split over workgroups; each writes an fp32 partial
 // (acc, m, l) in the split-KV layout and qp_merge_segments combines them (with the inverse rotation when asked).
 #include "qp_common.h"
@@ -465,8 +469,8 @@ __device__ __forceinline__ void pf_initial_max(PfRows<HS, NT> &r, const f32x4_t 
 //   phase A: S^T of tile i + 1 (K from kd1; 3 MFMAs per K operand, one per row tile)
 //            + softmax of tile i (scores sprev, scalars from vb0) + the K part of tile i + 2's unpack;
 //   phase B: O^T += V^T P^T of tile i (V^T from vb0) + the V part of tile i + 2's unpack.
-// Each phase is written as a sequence of MFMA steps, the operand loads three steps ahead and the VALU work spread
-// between them. The steps are not fenced: the compiler's own interleaving across steps measures 5 % faster than
+// Each phase is written as a sequence of MFMA steps, the operand loads four (K) or three (V^T) steps ahead and the
+// VALU work spread between them. The steps are not fenced: the compiler's own interleaving across steps measures 5 % faster than
 // sched_barrier fences after every step (4.09-4.15 against 4.37 ms on the 1024-token chunk over 131072 keys).
 // A row whose scores exceed the running maximum by more than the headroom raises its maximum there, in phase A: its
 // l and its accumulators are scaled down by the difference (rare; the tiles move through rescale_lds, a lane's 16 bytes
