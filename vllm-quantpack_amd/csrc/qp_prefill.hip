@@ -100,12 +100,10 @@ __device__ __forceinline__ void pf_runs(const PrefillParams &p, int k0, int kend
   b1 = uniform(fast_div(key1, p.bs_magic, p.bs_shift));
 }
 
-// One dwordx4 per lane from base + voff straight into LDS at dst + 16 * lane (global_load_lds_dwordx4 with a scalar
-// base: the lane offset is the only vector operand).
-__device__ __forceinline__ void dma16_run(const uint8_t *base, uint32_t voff, uint8_t *dst) {
+// One dwordx4 per lane from base + voff straight into LDS at byte address lds + 16 * lane (global_load_lds_dwordx4
+// with a scalar base: the lane offset is the only vector operand).
+__device__ __forceinline__ void dma16_run(const uint8_t *base, uint32_t voff, uint32_t lds) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  const uint32_t lds =
-      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)dst);
   // (readfirstlane returns a signed int: each half is widened as unsigned, or a low word with bit 31 set would
   // sign-extend over the high word)
   const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)base);
@@ -116,29 +114,57 @@ __device__ __forceinline__ void dma16_run(const uint8_t *base, uint32_t voff, ui
 #endif
 }
 
-// HBM -> LDS copies of a tile's two 16-cell page runs into its packed slot (run r's unit u at pk + 16 (r kRunUnits +
-// u)). Each run goes in kChunks copies of 64 units, the last one partial (lanes past the run do not copy), and copy q
-// of the tile's 2 kChunks goes to wave q % 4. A copy reads one run: the run's scalar base plus the lane's fixed
-// offset, so a tile costs the waves two run bases and one M0 per copy, and no per-lane address arithmetic.
+// HBM -> LDS copies of a tile's two 16-cell page runs into its packed slot (run r's unit u at LDS byte pk + 16 (r
+// kRunUnits + u)). The copies are numbered full ones first: q < kFull are run 0's 64-unit copies, then run 1's, then
+// the two runs' partial tails (lanes past the run do not copy); copy q goes to wave q % 4 as its (q / 4)-th. Slot i
+// of all four waves then reads one run whenever copies 4i .. 4i + 3 do (all of them for 16-cell int4 runs at head
+// 256), so that run's base is chosen at compile time. A copy reads one run: the run's scalar base plus the lane's
+// fixed offset, so a tile costs the waves two run bases and one M0 per copy, and no per-lane address arithmetic.
 template <class Sh>
 struct PfCopies {
-  static constexpr int kChunks = (Sh::kRunUnits + 63) / 64;
-  static constexpr int kTail = Sh::kRunUnits - 64 * (kChunks - 1);  // lanes of a run's last copy
-  static constexpr int kCopies = 2 * kChunks;
-  static constexpr int kMax = (kCopies + kPfWaves - 1) / kPfWaves;   // copies of the busiest wave per tile
-  int w, lane, n;                                                    // n: this wave's copies per tile
+  static constexpr int kFull = Sh::kRunUnits / 64;               // full copies of a run
+  static constexpr int kTail = Sh::kRunUnits % 64;               // lanes of a run's partial copy (0: none)
+  static constexpr int kCopies = 2 * kFull + (kTail ? 2 : 0);
+  static constexpr int kMax = (kCopies + kPfWaves - 1) / kPfWaves;  // copies of the busiest wave per tile
+  int w, lane, n;                                                   // n: this wave's copies per tile
 
   __device__ __forceinline__ PfCopies(int w_, int lane_)
       : w(w_), lane(lane_), n((kCopies - w_ + kPfWaves - 1) / kPfWaves) {}
 
-  __device__ __forceinline__ void issue(const uint8_t *base0, const uint8_t *base1, uint8_t *pk) const {
+  static constexpr __host__ __device__ int run_of(int q) { return q < kFull ? 0 : q < 2 * kFull ? 1 : q - 2 * kFull; }
+  static constexpr __host__ __device__ int unit_of(int q) { return q < 2 * kFull ? 64 * (q % kFull) : 64 * kFull; }
+  // the run that every copy of slot i reads, or -1 when they read both (the tails follow all full copies, so a slot
+  // can hold copies of run 1 between two of run 0)
+  static constexpr __host__ __device__ int slot_run(int i) {
+    int r = run_of(kPfWaves * i);
+    for (int q = kPfWaves * i + 1; q < kPfWaves * (i + 1) && q < kCopies; ++q)
+      if (run_of(q) != r) r = -1;
+    return r;
+  }
+  // every unit of both runs is copied exactly once, and a one-run slot holds copies of that run only
+  static constexpr __host__ __device__ bool plan_ok() {
+    for (int r = 0; r < 2; ++r)
+      for (int u = 0; u < Sh::kRunUnits; ++u) {
+        int n = 0;
+        for (int q = 0; q < kCopies; ++q)
+          if (run_of(q) == r && u >= unit_of(q) && u < unit_of(q) + (q < 2 * kFull ? 64 : kTail)) ++n;
+        if (n != 1) return false;
+      }
+    for (int i = 0; i < kMax; ++i)
+      for (int q = kPfWaves * i; q < kPfWaves * (i + 1) && q < kCopies; ++q)
+        if (slot_run(i) >= 0 && run_of(q) != slot_run(i)) return false;
+    return true;
+  }
+
+  __device__ __forceinline__ void issue(const uint8_t *base0, const uint8_t *base1, uint32_t pk) const {
+    static_assert(plan_ok(), "the copies must cover both runs exactly once");
 #pragma unroll
     for (int i = 0; i < kMax; ++i) {
       const int q = kPfWaves * i + w;
-      if (i + 1 < kMax || q < kCopies) {  // wave-uniform
-        const int r = q / kChunks, c = q % kChunks;
-        const int u = 64 * c;  // first unit of the copy within its run
-        if (kTail == 64 || c + 1 < kChunks || lane < kTail)
+      if (kPfWaves * (i + 1) <= kCopies || q < kCopies) {  // wave-uniform (always true for a full slot)
+        const int r = slot_run(i) >= 0 ? slot_run(i) : run_of(q);  // a constant when the slot reads one run
+        const int u = unit_of(q);                                          // first unit of the copy within its run
+        if (kPfWaves * i + kPfWaves <= 2 * kFull || q < 2 * kFull || lane < kTail)  // full copies: no lane mask
           dma16_run(r ? base1 : base0, 16 * (u + lane), pk + 16 * (r * Sh::kRunUnits + u));
       }
     }
@@ -163,12 +189,21 @@ struct PfRunBases {
   }
 };
 
-template <class Sh>
+// Tiles start at multiples of 32 keys (splits are whole 32-key tiles), so with 16-token blocks (BS16) the runs of
+// tile k0 are the whole blocks k0 / 16 and k0 / 16 + 1 (the first again when the second starts past kend).
+template <class Sh, bool BS16>
 __device__ __forceinline__ void pf_slots(const PrefillParams &p, int k0, int kend, PfRunBases &rb, int &b0, int &b1) {
-  int key1;
-  pf_runs(p, k0, kend, key1, b0, b1);
-  rb.soff0 = uniform((k0 - b0 * p.block_size) * Sh::kCell);
-  rb.soff1 = uniform((key1 - b1 * p.block_size) * Sh::kCell);
+  if constexpr (BS16) {
+    b0 = uniform(k0 >> 4);
+    b1 = uniform(k0 + 16 < kend ? b0 + 1 : b0);
+    rb.soff0 = 0;
+    rb.soff1 = 0;
+  } else {
+    int key1;
+    pf_runs(p, k0, kend, key1, b0, b1);
+    rb.soff0 = uniform((k0 - b0 * p.block_size) * Sh::kCell);
+    rb.soff1 = uniform((key1 - b1 * p.block_size) * Sh::kCell);
+  }
 }
 
 // Strided fallback: the same packed image gathered dword by dword through VGPRs (any 4-byte aligned views).
@@ -630,7 +665,7 @@ __device__ __forceinline__ void rotate_out_row(float (&x)[HS / 4], const float *
   }
 }
 
-template <int HS, int KFMT, int NT, bool SPAN>
+template <int HS, int KFMT, int NT, bool SPAN, bool BS16>
 __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillParams p) {
   using Sh = PfShape<HS, KFMT>;
   using St = PfStager<HS, KFMT>;
@@ -665,7 +700,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
   const int S = p.num_splits;
   const int seg = (n + S * QP_DECODE_TILE - 1) / (S * QP_DECODE_TILE) * QP_DECODE_TILE;
   const int kb = split * seg;
-  const int ke = min(kend, kb + seg);
+  const int ke = uniform(min(kend, kb + seg));
   if (S > 1 && kb >= n) return;  // inactive segment: the merge does not read it
 
   // ---- the wave's row tiles: tile tt = w + 4 jt is (query head tt % G, tokens 16 (tt / G) .. + 15 of the block)
@@ -709,6 +744,8 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
 
   // tile t: packed slot t % 3, K buffer t % 2, V buffer t % 3
   auto pk_of = [&](int t) { return smem + (t % 3) * Sh::kPk; };
+  const uint32_t lds0 = uniform((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)smem);
+  auto pk_lds_of = [&](int t) { return lds0 + (uint32_t)((t % 3) * Sh::kPk); };
   auto kd_of = [&](int t) { return smem + Sh::kOffK + (t & 1) * Sh::kKd; };
   auto vb_of = [&](int t) { return smem + Sh::kOffV + (t % 3) * Sh::kVb; };
   auto tile_key = [&](int t) { return kb + t * kPfKeys; };
@@ -719,9 +756,9 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
     if constexpr (SPAN) {
       PfRunBases rb;
       int b0, b1;
-      pf_slots<Sh>(p, tile_key(t), ke, rb, b0, b1);
+      pf_slots<Sh, BS16>(p, tile_key(t), ke, rb, b0, b1);
       table_pair(trow, b0, b1, rb.bid0, rb.bid1);
-      copies.issue(rb.base0(hbase, ks0), rb.base1(hbase, ks0), pk_of(t));
+      copies.issue(rb.base0(hbase, ks0), rb.base1(hbase, ks0), pk_lds_of(t));
     } else {
       pf_gather<Sh>(p, trow, tile_key(t), ke, h, pk_of(t));
     }
@@ -770,11 +807,24 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
     // compiler issues s_load and places the lgkm wait itself, and the vm counter of the copies is left alone)
     const __attribute__((address_space(4))) int32_t *ctab = (const __attribute__((address_space(4))) int32_t *)trow;
     PfRunBases ahead{};
+    // with 16-token blocks the tiles' table entries are consecutive pairs: a pointer steps two entries per tile
+    // (table_ahead is called for tiles 4, 5, 6, ... in order)
+    const __attribute__((address_space(4))) int32_t *tnext = ctab + (kb >> 4) + 8;
     auto table_ahead = [&](int t) {
-      int b0, b1;
-      pf_slots<Sh>(p, tile_key(t), ke, ahead, b0, b1);
-      ahead.bid0 = ctab[b0];
-      ahead.bid1 = ctab[b1];
+      if constexpr (BS16) {
+        ahead.bid0 = tnext[0];
+        // the second run only if it starts before ke (a byte offset of 0 or 4: the load takes it as its SGPR offset)
+        const uint32_t off1 = (uint32_t)min(4, ((ke - 1 - tile_key(t)) >> 4) << 2);
+        ahead.bid1 = *(const __attribute__((address_space(4))) int32_t *)((const __attribute__((address_space(4))) uint8_t *)tnext + off1);
+        ahead.soff0 = 0;
+        ahead.soff1 = 0;
+        tnext += 2;
+      } else {
+        int b0, b1;
+        pf_slots<Sh, false>(p, tile_key(t), ke, ahead, b0, b1);
+        ahead.bid0 = ctab[b0];
+        ahead.bid1 = ctab[b1];
+      }
     };
     if (SPAN && ntiles > 4) table_ahead(4);
     // A rescale parks each accumulator tile in 16 bytes of its lane inside the padding at the end of the V^T rows of
@@ -792,6 +842,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
       constexpr bool kMask = decltype(mask_tag)::value;
       constexpr int PH = decltype(phase_tag)::value;  // it % 6, or -1 when not known
       auto pk_at = [&](int k) { return PH >= 0 ? smem + ((PH + k) % 3) * Sh::kPk : pk_of(it + k); };
+      auto pk_lds_at = [&](int k) { return PH >= 0 ? lds0 + (uint32_t)(((PH + k) % 3) * Sh::kPk) : pk_lds_of(it + k); };
       auto kd_at = [&](int k) { return PH >= 0 ? smem + Sh::kOffK + ((PH + k) & 1) * Sh::kKd : kd_of(it + k); };
       auto vb_at = [&](int k) { return PH >= 0 ? smem + Sh::kOffV + ((PH + k) % 3) * Sh::kVb : vb_of(it + k); };
       if constexpr (SPAN) {
@@ -801,7 +852,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
       __syncthreads();  // tile it + 1 unpacked by all; tile it + 2 landed; tile it's K and it - 1's V buffers free
       if (it + 4 < ntiles) {  // into slot (it + 1) % 3, unpacked before this barrier
         if constexpr (SPAN) {
-          copies.issue(ahead.base0(hbase, ks0), ahead.base1(hbase, ks0), pk_at(4));
+          copies.issue(ahead.base0(hbase, ks0), ahead.base1(hbase, ks0), pk_lds_at(4));
           if (it + 5 < ntiles) table_ahead(it + 5);
         } else {
           fetch(it + 4);
@@ -936,8 +987,9 @@ int64_t partial_bytes(const qp_paged_cache *cache, const qp_prefill_args *a, int
 
 template <int HS, int KFMT, int NT>
 void launch_prefill(const PrefillParams &p, dim3 grid, bool span, hipStream_t s) {
-  if (span) prefill_kernel<HS, KFMT, NT, true><<<grid, kPfWaves * 64, 0, s>>>(p);
-  else prefill_kernel<HS, KFMT, NT, false><<<grid, kPfWaves * 64, 0, s>>>(p);
+  if (span && p.block_size == 16) prefill_kernel<HS, KFMT, NT, true, true><<<grid, kPfWaves * 64, 0, s>>>(p);
+  else if (span) prefill_kernel<HS, KFMT, NT, true, false><<<grid, kPfWaves * 64, 0, s>>>(p);
+  else prefill_kernel<HS, KFMT, NT, false, false><<<grid, kPfWaves * 64, 0, s>>>(p);
 }
 
 template <int HS, int KFMT>
