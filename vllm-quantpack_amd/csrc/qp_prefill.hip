@@ -118,27 +118,31 @@ __device__ __forceinline__ void dma16_run(const uint8_t *base, uint32_t voff, ui
 // kRunUnits + u)). The copies are numbered full ones first: q < kFull are run 0's 64-unit copies, then run 1's, then
 // the two runs' partial tails (lanes past the run do not copy); copy q goes to wave q % 4 as its (q / 4)-th. Slot i
 // of all four waves then reads one run whenever copies 4i .. 4i + 3 do (all of them for 16-cell int4 runs at head
-// 256), so that run's base is chosen at compile time. A copy reads one run: the run's scalar base plus the lane's
-// fixed offset, so a tile costs the waves two run bases and one M0 per copy, and no per-lane address arithmetic.
+// 256), so that run's base is chosen at compile time. Waves whose last slot is past the plan copy one of the last
+// copies again (the same bytes to the same place, complete before the barrier that follows their wait): every wave
+// then issues kMax copies per tile and waits on a count fixed at compile time. A copy reads one run: the run's
+// scalar base plus the lane's fixed offset, so a tile costs the waves two run bases and one M0 per copy, and no
+// per-lane address arithmetic.
 template <class Sh>
 struct PfCopies {
   static constexpr int kFull = Sh::kRunUnits / 64;               // full copies of a run
   static constexpr int kTail = Sh::kRunUnits % 64;               // lanes of a run's partial copy (0: none)
   static constexpr int kCopies = 2 * kFull + (kTail ? 2 : 0);
   static constexpr int kMax = (kCopies + kPfWaves - 1) / kPfWaves;  // copies of the busiest wave per tile
-  int w, lane, n;                                                   // n: this wave's copies per tile
+  int w, lane;
 
-  __device__ __forceinline__ PfCopies(int w_, int lane_)
-      : w(w_), lane(lane_), n((kCopies - w_ + kPfWaves - 1) / kPfWaves) {}
+  __device__ __forceinline__ PfCopies(int w_, int lane_) : w(w_), lane(lane_) {}
 
+  // the copy a wave issues as q: past the plan, one of its last copies again
+  static constexpr __host__ __device__ int copy_of(int q) { return q < kCopies ? q : 2 * kCopies - 1 - q; }
   static constexpr __host__ __device__ int run_of(int q) { return q < kFull ? 0 : q < 2 * kFull ? 1 : q - 2 * kFull; }
   static constexpr __host__ __device__ int unit_of(int q) { return q < 2 * kFull ? 64 * (q % kFull) : 64 * kFull; }
   // the run that every copy of slot i reads, or -1 when they read both (the tails follow all full copies, so a slot
   // can hold copies of run 1 between two of run 0)
   static constexpr __host__ __device__ int slot_run(int i) {
-    int r = run_of(kPfWaves * i);
-    for (int q = kPfWaves * i + 1; q < kPfWaves * (i + 1) && q < kCopies; ++q)
-      if (run_of(q) != r) r = -1;
+    int r = run_of(copy_of(kPfWaves * i));
+    for (int q = kPfWaves * i + 1; q < kPfWaves * (i + 1); ++q)
+      if (run_of(copy_of(q)) != r) r = -1;
     return r;
   }
   // every unit of both runs is copied exactly once, and a one-run slot holds copies of that run only
@@ -151,8 +155,9 @@ struct PfCopies {
         if (n != 1) return false;
       }
     for (int i = 0; i < kMax; ++i)
-      for (int q = kPfWaves * i; q < kPfWaves * (i + 1) && q < kCopies; ++q)
-        if (slot_run(i) >= 0 && run_of(q) != slot_run(i)) return false;
+      for (int q = kPfWaves * i; q < kPfWaves * (i + 1); ++q)
+        if (copy_of(q) < 0 || copy_of(q) >= kCopies || (slot_run(i) >= 0 && run_of(copy_of(q)) != slot_run(i)))
+          return false;
     return true;
   }
 
@@ -160,20 +165,17 @@ struct PfCopies {
     static_assert(plan_ok(), "the copies must cover both runs exactly once");
 #pragma unroll
     for (int i = 0; i < kMax; ++i) {
-      const int q = kPfWaves * i + w;
-      if (kPfWaves * (i + 1) <= kCopies || q < kCopies) {  // wave-uniform (always true for a full slot)
-        const int r = slot_run(i) >= 0 ? slot_run(i) : run_of(q);  // a constant when the slot reads one run
-        const int u = unit_of(q);                                          // first unit of the copy within its run
-        if (kPfWaves * i + kPfWaves <= 2 * kFull || q < 2 * kFull || lane < kTail)  // full copies: no lane mask
-          dma16_run(r ? base1 : base0, 16 * (u + lane), pk + 16 * (r * Sh::kRunUnits + u));
-      }
+      const int q = copy_of(kPfWaves * i + w);
+      const int r = slot_run(i) >= 0 ? slot_run(i) : run_of(q);  // a constant when the slot reads one run
+      const int u = unit_of(q);                                   // first unit of the copy within its run
+      if (kPfWaves * i + kPfWaves <= 2 * kFull || q < 2 * kFull || lane < kTail)  // full copies: no lane mask
+        dma16_run(r ? base1 : base0, 16 * (u + lane), pk + 16 * (r * Sh::kRunUnits + u));
     }
   }
   // waits until at most K tiles' copies of this wave are outstanding
   template <int K>
   __device__ __forceinline__ void wait() const {
-    if (n == kMax) wait_vmcnt<K * kMax>();
-    else wait_vmcnt<K * (kMax - 1)>();
+    wait_vmcnt<K * kMax>();
   }
 };
 
@@ -532,7 +534,7 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
   auto vaddr = [&](int b) { return vb0 + (16 * b + col) * Sh::kVtRow + 16 * g; };
   bf16x8_t kbuf[kPre], vbuf[kPreV];
   float4 ka[2], ke[2], ks[2];
-  float t[NT][2][4], lsum[NT];
+  float t[NT][2][4];
   u32x4_t pop[NT];
 
   // softmax of row tile j, item k: 0-1 scores of sub-tile k, 2 the headroom check, 3-6 probabilities of 2 keys
@@ -567,14 +569,12 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
           for (int jj = 0; jj < 4; ++jj) t[j][sb][jj] -= up;
         scale_agpr<17, HS / 16 + 1>(r.acc[j], alpha, rescale_lds);
       }
-      lsum[j] = 0.f;
     } else {
       const int sub = (k - 3) >> 1, h2 = (k - 3) & 1;
       const float p0 = __builtin_amdgcn_exp2f(t[j][sub][2 * h2]);
       const float p1 = __builtin_amdgcn_exp2f(t[j][sub][2 * h2 + 1]);
-      lsum[j] += p0 + p1;
+      r.l[j] += p0 + p1;  // after any rescale of l in item 2
       pop[j][2 * sub + h2] = pack_bf16x2(p0 * ks[sub][2 * h2], p1 * ks[sub][2 * h2 + 1]);
-      if (k == kSm - 1) r.l[j] += lsum[j];
     }
   };
 
@@ -810,11 +810,13 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
     // with 16-token blocks the tiles' table entries are consecutive pairs: a pointer steps two entries per tile
     // (table_ahead is called for tiles 4, 5, 6, ... in order)
     const __attribute__((address_space(4))) int32_t *tnext = ctab + (kb >> 4) + 8;
-    auto table_ahead = [&](int t) {
+    auto table_ahead = [&](int t, auto steady_tag) {
       if constexpr (BS16) {
         ahead.bid0 = tnext[0];
-        // the second run only if it starts before ke (a byte offset of 0 or 4: the load takes it as its SGPR offset)
-        const uint32_t off1 = (uint32_t)min(4, ((ke - 1 - tile_key(t)) >> 4) << 2);
+        // the second run only if it starts before ke (a byte offset of 0 or 4: the load takes it as its SGPR offset);
+        // a steady iteration's tile is followed by others, so its second run always does
+        const uint32_t off1 =
+            decltype(steady_tag)::value ? 4u : (uint32_t)min(4, ((ke - 1 - tile_key(t)) >> 4) << 2);
         ahead.bid1 = *(const __attribute__((address_space(4))) int32_t *)((const __attribute__((address_space(4))) uint8_t *)tnext + off1);
         ahead.soff0 = 0;
         ahead.soff1 = 0;
@@ -826,7 +828,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
         ahead.bid1 = ctab[b1];
       }
     };
-    if (SPAN && ntiles > 4) table_ahead(4);
+    if (SPAN && ntiles > 4) table_ahead(4, std::false_type{});
     // A rescale parks each accumulator tile in 16 bytes of its lane inside the padding at the end of the V^T rows of
     // the first V buffer: no copy, stager store or MFMA operand read touches those bytes, so no wave can collide there.
     static_assert(Sh::kVtRow - kPfKeys * 2 >= 32 && 128 <= Sh::kVtRows, "two 16-byte pad slots per V^T row");
@@ -837,23 +839,25 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
     // One pipeline iteration. Tiles whose keys are all visible to every row come first and run without the causal
     // mask; the rest (the chunk's own keys) run with it.
     // With the phase it % 6 known at compile time (the unrolled loop below), every buffer of the iteration sits at a
-    // constant LDS offset, so the ds instructions take it as an immediate instead of per-tile address arithmetic.
+    // constant LDS offset, so the ds instructions take it as an immediate instead of per-tile address arithmetic; that
+    // loop also stops 11 tiles before the end, so its iterations skip the end-of-split checks (kSteady).
     auto iteration = [&](int it, auto mask_tag, auto phase_tag) {
       constexpr bool kMask = decltype(mask_tag)::value;
       constexpr int PH = decltype(phase_tag)::value;  // it % 6, or -1 when not known
+      constexpr bool kSteady = PH >= 0;                // it + 5 < ntiles
       auto pk_at = [&](int k) { return PH >= 0 ? smem + ((PH + k) % 3) * Sh::kPk : pk_of(it + k); };
       auto pk_lds_at = [&](int k) { return PH >= 0 ? lds0 + (uint32_t)(((PH + k) % 3) * Sh::kPk) : pk_lds_of(it + k); };
       auto kd_at = [&](int k) { return PH >= 0 ? smem + Sh::kOffK + ((PH + k) & 1) * Sh::kKd : kd_of(it + k); };
       auto vb_at = [&](int k) { return PH >= 0 ? smem + Sh::kOffV + ((PH + k) % 3) * Sh::kVb : vb_of(it + k); };
       if constexpr (SPAN) {
-        if (it + 3 < ntiles) copies.template wait<1>();
+        if (kSteady || it + 3 < ntiles) copies.template wait<1>();
         else wait_vmcnt<0>();
       }
       __syncthreads();  // tile it + 1 unpacked by all; tile it + 2 landed; tile it's K and it - 1's V buffers free
-      if (it + 4 < ntiles) {  // into slot (it + 1) % 3, unpacked before this barrier
+      if (kSteady || it + 4 < ntiles) {  // into slot (it + 1) % 3, unpacked before this barrier
         if constexpr (SPAN) {
           copies.issue(ahead.base0(hbase, ks0), ahead.base1(hbase, ks0), pk_lds_at(4));
-          if (it + 5 < ntiles) table_ahead(it + 5);
+          if (kSteady || it + 5 < ntiles) table_ahead(it + 5, std::integral_constant<bool, kSteady>{});
         } else {
           fetch(it + 4);
         }
@@ -880,7 +884,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
     // int4 keys only: with int8 keys the unrolled loop's extra live addresses spill 160 bytes per lane and measured
     // 2 % slower (4.47 against 4.37 ms), while int4 keys gain 5 % (3.75 against 3.93 ms)
     if constexpr (SPAN && KFMT == QP_CODES_INT4) {
-      for (; it + 6 <= nplain; it += 6) {
+      for (; it + 6 <= nplain && it + 11 <= ntiles; it += 6) {  // iterations it .. it + 5 are steady
         iteration(it, std::false_type{}, std::integral_constant<int, 0>{});
         iteration(it + 1, std::false_type{}, std::integral_constant<int, 1>{});
         iteration(it + 2, std::false_type{}, std::integral_constant<int, 2>{});
