@@ -321,29 +321,34 @@ __device__ __forceinline__ float2 value_floats_paired(uint32_t word, bool ok) {
   return make_float2(ok ? __uint_as_float(word & 0xFFFFFFF0u) : 0.f, __uint_as_float(pair));
 }
 
-// One dwordx4 per lane straight from HBM into LDS at dst + 16 * lane (global_load_lds_dwordx4, LDS base in M0).
-// Issued as inline assembly so that the compiler does not order its own LDS stores behind these copies: every wait
-// on them is placed by hand (wait_vmcnt before a stage is read, wait_lgkm0 before a stage is refilled).
-__device__ __forceinline__ void dma16(const uint8_t *src, uint8_t *dst) {
+// One dwordx4 per lane from base + voff straight into LDS at byte address lds + 16 * lane (global_load_lds_dwordx4
+// in its scalar-base form: the lane offset is the only vector operand, so a run of copies from one base costs no
+// per-lane address arithmetic). Issued as inline assembly so that the compiler does not order its own LDS stores
+// behind these copies: every wait on them is placed by hand (wait_vmcnt before a stage is read, wait_lgkm0 before a
+// stage is refilled). NT adds the nontemporal hint, for data read exactly once per launch (the decode stream of the
+// KV cache): it streams through the caches instead of displacing what is reused, and measured about 13 % more
+// bandwidth from HBM.
+template <bool NT>
+__device__ __forceinline__ void dma16_saddr(const uint8_t *base, uint32_t voff, uint32_t lds) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  // readfirstlane right at the use: the LDS base is uniform, and an SGPR defined here cannot have been spilled to a
-  // VGPR on the way (the "s" operand must be an SGPR)
-  const uint32_t lds =
-      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)dst);
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
-               : "memory", "m0");
+  // (readfirstlane returns a signed int: each half is widened as unsigned, or a low word with bit 31 set would
+  // sign-extend over the high word)
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)base);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)((uintptr_t)base >> 32));
+  const uint64_t b = ((uint64_t)hi << 32) | (uint64_t)lo;
+  if constexpr (NT)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(b), "s"(lds)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(b), "s"(lds)
+                 : "memory", "m0");
 #endif
 }
 
-// dma16 with the nontemporal hint, for data read exactly once per launch (the decode stream of the KV cache): it
-// streams through the caches instead of displacing what is reused, and measures about 13 % more bandwidth from HBM.
-__device__ __forceinline__ void dma16_stream(const uint8_t *src, uint8_t *dst) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  const uint32_t lds =
-      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)dst);
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(lds)
-               : "memory", "m0");
-#endif
+// LDS byte address of a pointer into shared memory, wave-uniform
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p);
 }
 
 // Two block-table entries through the scalar cache (s_load, lgkm counter). A vector load here would be ordered

@@ -871,16 +871,19 @@ __device__ __forceinline__ void issue_span_dma(const DecodeParams &p, const int3
     bidx[hc] = uniform(fast_div(pos[hc], p.bs_magic, p.bs_shift));
   }
   table_pair(trow, bidx[0], bidx[1], bid[0], bid[1]);
+  // each half is one contiguous run: a scalar base and the lanes' fixed offsets (nontemporal: the stream is read once)
+  const uint32_t lds = lds_addr(stage);
 #pragma unroll
   for (int hc = 0; hc < 2; ++hc) {
     const int slot0 = pos[hc] - bidx[hc] * p.block_size;
-    const uint8_t *src =
-        p.kcodes + (int64_t)bid[hc] * p.ks0 + (int64_t)h * p.ks2 + (int64_t)slot0 * Sh::kCell + 16 * lane;
-    uint8_t *dst = stage + hc * Sh::kHalf;
+    // (block ids and slots are non-negative: unsigned products need no sign handling)
+    const uint8_t *base = p.kcodes + (int64_t)h * p.ks2 + (uint64_t)(uint32_t)bid[hc] * (uint64_t)p.ks0 +
+                          (uint32_t)slot0 * (uint32_t)Sh::kCell;
 #pragma unroll
-    for (int i = 0; i < Sh::kFull; ++i) dma16_stream(src + 1024 * i, dst + 1024 * i);
+    for (int i = 0; i < Sh::kFull; ++i)
+      dma16_saddr<true>(base, 16 * lane + 1024 * i, lds + hc * Sh::kHalf + 1024 * i);
     if constexpr (Sh::kRem != 0) {
-      if (lane < Sh::kRem) dma16_stream(src + 1024 * Sh::kFull, dst + 1024 * Sh::kFull);
+      if (lane < Sh::kRem) dma16_saddr<true>(base, 16 * lane + 1024 * Sh::kFull, lds + hc * Sh::kHalf + 1024 * Sh::kFull);
     }
   }
 }

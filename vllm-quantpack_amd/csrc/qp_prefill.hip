@@ -100,20 +100,6 @@ __device__ __forceinline__ void pf_runs(const PrefillParams &p, int k0, int kend
   b1 = uniform(fast_div(key1, p.bs_magic, p.bs_shift));
 }
 
-// One dwordx4 per lane from base + voff straight into LDS at byte address lds + 16 * lane (global_load_lds_dwordx4
-// with a scalar base: the lane offset is the only vector operand).
-__device__ __forceinline__ void dma16_run(const uint8_t *base, uint32_t voff, uint32_t lds) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  // (readfirstlane returns a signed int: each half is widened as unsigned, or a low word with bit 31 set would
-  // sign-extend over the high word)
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)base);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)((uintptr_t)base >> 32));
-  const uint64_t b = ((uint64_t)hi << 32) | (uint64_t)lo;
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(b), "s"(lds)
-               : "memory", "m0");
-#endif
-}
-
 // HBM -> LDS copies of a tile's two 16-cell page runs into its packed slot (run r's unit u at LDS byte pk + 16 (r
 // kRunUnits + u)). The copies are numbered full ones first: q < kFull are run 0's 64-unit copies, then run 1's, then
 // the two runs' partial tails (lanes past the run do not copy); copy q goes to wave q % 4 as its (q / 4)-th. Slot i
@@ -169,7 +155,7 @@ struct PfCopies {
       const int r = slot_run(i) >= 0 ? slot_run(i) : run_of(q);  // a constant when the slot reads one run
       const int u = unit_of(q);                                   // first unit of the copy within its run
       if (kPfWaves * i + kPfWaves <= 2 * kFull || q < 2 * kFull || lane < kTail)  // full copies: no lane mask
-        dma16_run(r ? base1 : base0, 16 * (u + lane), pk + 16 * (r * Sh::kRunUnits + u));
+        dma16_saddr<false>(r ? base1 : base0, 16 * (u + lane), pk + 16 * (r * Sh::kRunUnits + u));
     }
   }
   // waits until at most K tiles' copies of this wave are outstanding
