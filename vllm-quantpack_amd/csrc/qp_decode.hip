@@ -864,21 +864,27 @@ template <class Sh>
 __device__ __forceinline__ void issue_span_dma(const DecodeParams &p, const int32_t *trow, int k0, int kend, int h,
                                                int lane, uint8_t *stage) {
   // a half at or past kend re-reads half 0 (valid memory) so that every chunk issues the same count of loads
-  int pos[2], bidx[2], bid[2];
+  int bidx[2], slot[2], bid[2];
+  if (p.block_size == 16) {  // chunks start at multiples of 32 keys: each half is a whole block
+    bidx[0] = uniform(k0 >> 4);
+    bidx[1] = uniform(k0 + 16 < kend ? bidx[0] + 1 : bidx[0]);
+    slot[0] = slot[1] = 0;
+  } else {
 #pragma unroll
-  for (int hc = 0; hc < 2; ++hc) {
-    pos[hc] = uniform(k0 + 16 * ((k0 + 16 * hc < kend) ? hc : 0));
-    bidx[hc] = uniform(fast_div(pos[hc], p.bs_magic, p.bs_shift));
+    for (int hc = 0; hc < 2; ++hc) {
+      const int pos = uniform(k0 + 16 * ((k0 + 16 * hc < kend) ? hc : 0));
+      bidx[hc] = uniform(fast_div(pos, p.bs_magic, p.bs_shift));
+      slot[hc] = pos - bidx[hc] * p.block_size;
+    }
   }
   table_pair(trow, bidx[0], bidx[1], bid[0], bid[1]);
   // each half is one contiguous run: a scalar base and the lanes' fixed offsets (nontemporal: the stream is read once)
   const uint32_t lds = lds_addr(stage);
 #pragma unroll
   for (int hc = 0; hc < 2; ++hc) {
-    const int slot0 = pos[hc] - bidx[hc] * p.block_size;
     // (block ids and slots are non-negative: unsigned products need no sign handling)
     const uint8_t *base = p.kcodes + (int64_t)h * p.ks2 + (uint64_t)(uint32_t)bid[hc] * (uint64_t)p.ks0 +
-                          (uint32_t)slot0 * (uint32_t)Sh::kCell;
+                          (uint32_t)slot[hc] * (uint32_t)Sh::kCell;
 #pragma unroll
     for (int i = 0; i < Sh::kFull; ++i)
       dma16_saddr<true>(base, 16 * lane + 1024 * i, lds + hc * Sh::kHalf + 1024 * i);
