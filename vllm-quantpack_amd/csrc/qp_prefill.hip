@@ -325,6 +325,7 @@ struct PfStager {
   const uint8_t *pk;
   uint8_t *kd, *vt;
   int k0, kend, tid;
+  bool full;  // every key of the tile is below kend
   float scale_log2;
   uint32_t kx[kNK];
   uint32_t vx[8], pr[4];
@@ -372,7 +373,7 @@ struct PfStager {
   }
   __device__ __forceinline__ void s_store() {
     const int kk = tid & (kPfKeys - 1);
-    const bool ok = k0 + kk < kend;
+    const bool ok = full || k0 + kk < kend;
     float a, e;
     if constexpr (KFMT == QP_CODES_INT4) {
       a = __uint_as_float(kw & 0xFFFFFFF0u) * scale_log2;
@@ -853,6 +854,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
       st.pk = pk_at(2);
       st.kd = kd_at(2);
       st.vt = vb_at(2);
+      st.full = kSteady;  // a steady iteration's tile it + 2 is followed by others
       st.k0 = tile_key(it + 2);
       st.kend = ke;
       st.tid = tid;
