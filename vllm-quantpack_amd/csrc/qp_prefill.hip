@@ -78,7 +78,14 @@ struct PfShape {
   static constexpr int kRunUnits = kCell;  // 16-byte units of one 16-cell page run
   static constexpr int kTileUnits = 2 * kRunUnits;
   static constexpr int kPk = (kTileUnits + kPfWaves * 64 - 1) / (kPfWaves * 64) * kPfWaves * 1024;  // packed slot
-  static constexpr int kKdRow = HS * 2 + 16;                 // bf16 K row, padded: conflict-free 16 B reads
+  static constexpr int kKdRow = HS * 2 + 16;                 // bf16 K row, padded by one 16-byte unit
+  // Where a K row's 16-byte chunk c (channels 8c .. 8c + 7 in operand order) sits. An operand read has lane group g
+  // (lanes 16 g .. 16 g + 15, keys 0..15) read chunk 8 g + s at step s, and the LDS serves 32 lanes at a time from 128
+  // banks: with the one-unit padding, groups 0 and 1 (and 2 and 3) then meet in half of the banks. At head 256 the
+  // chunks of groups 1 and 2 trade places, so the two groups read 16 units apart and never meet.
+  static constexpr __host__ __device__ int kd_unit(int c) {
+    return HS == 256 ? (c & 7) | ((c & 8) << 1) | ((c & 16) >> 1) : c;
+  }
   static constexpr int kVtRow = kPfKeys * 2 + 32;            // bf16 V^T row (padding 32 B: 4 % faster than 16 B)
   static constexpr int kVtRows = HS + 16;                    // + the zero-point tile
   static constexpr int kKd = kPfKeys * kKdRow;               // one K buffer
@@ -241,7 +248,7 @@ __device__ __forceinline__ void pf_unpack_k(const uint8_t *pk, uint8_t *kd, int 
       const uint32_t x = *reinterpret_cast<const uint32_t *>(pk + kk * Sh::kCell + 4 * d);
       const uint32_t y = x >> 4;
       // channel order within the 8: (c0, c4, c1, c5, c2, c6, c3, c7), matching the query operand
-      *reinterpret_cast<u32x4_t *>(kd + kk * Sh::kKdRow + 16 * d) =
+      *reinterpret_cast<u32x4_t *>(kd + kk * Sh::kKdRow + 16 * Sh::kd_unit(d)) =
           u32x4_t{nib_pair(x), nib_pair(y), nib_pair(x >> 8), nib_pair(y >> 8)};
     }
   } else {
@@ -251,7 +258,7 @@ __device__ __forceinline__ void pf_unpack_k(const uint8_t *pk, uint8_t *kd, int 
       const int u = tid + kPfWaves * 64 * i;
       const int kk = u / kDw, d = u % kDw;
       const uint32_t x = *reinterpret_cast<const uint32_t *>(pk + kk * Sh::kCell + 4 * d);
-      *reinterpret_cast<u32x2_t *>(kd + kk * Sh::kKdRow + 8 * d) = i8_quad_bf16(x);
+      *reinterpret_cast<u32x2_t *>(kd + kk * Sh::kKdRow + 16 * Sh::kd_unit(d >> 1) + 8 * (d & 1)) = i8_quad_bf16(x);
     }
   }
 }
@@ -341,10 +348,10 @@ struct PfStager {
     const uint32_t x = kx[i];
     if constexpr (KFMT == QP_CODES_INT4) {
       const uint32_t y = x >> 4;
-      *reinterpret_cast<u32x4_t *>(kd + kk * Sh::kKdRow + 16 * d) =
+      *reinterpret_cast<u32x4_t *>(kd + kk * Sh::kKdRow + 16 * Sh::kd_unit(d)) =
           u32x4_t{nib_pair(x), nib_pair(y), nib_pair(x >> 8), nib_pair(y >> 8)};
     } else {
-      *reinterpret_cast<u32x2_t *>(kd + kk * Sh::kKdRow + 8 * d) = i8_quad_bf16(x);
+      *reinterpret_cast<u32x2_t *>(kd + kk * Sh::kKdRow + 16 * Sh::kd_unit(d >> 1) + 8 * (d & 1)) = i8_quad_bf16(x);
     }
   }
   // V unit (q4, ko) = tid mod HS (with HS = 128 the upper half repeats the lower half's unit: same bytes, same place)
@@ -451,7 +458,7 @@ __device__ __forceinline__ void pf_qk_tile(const PfRows<HS, NT> &r, const uint8_
   using Sh = PfShape<HS, KFMT>;
 #pragma unroll
   for (int sub = 0; sub < 2; ++sub) {
-    const uint8_t *kr = kd + (16 * sub + col) * Sh::kKdRow + 2 * (HS / 4) * g;
+    const uint8_t *kr = kd + (16 * sub + col) * Sh::kKdRow + 16 * Sh::kd_unit((HS / 32) * g);
 #pragma unroll
     for (int mi = 0; mi < HS / 32; ++mi) {
       const bf16x8_t kop = *reinterpret_cast<const bf16x8_t *>(kr + 16 * mi);
@@ -517,7 +524,10 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
   static_assert(St::kNK + kLag <= kQ, "K unpack stages must fit phase A");
   const float *kf = reinterpret_cast<const float *>(vb0 + Sh::kVt);
 
-  auto kaddr = [&](int s) { return kd1 + (16 * (s / kMi) + col) * Sh::kKdRow + 2 * (HS / 4) * g + 16 * (s % kMi); };
+  // (kd_unit leaves the low three bits of a chunk index alone: step s % kMi adds 16 (s % kMi) bytes to the lane base)
+  auto kaddr = [&](int s) {
+    return kd1 + (16 * (s / kMi) + col) * Sh::kKdRow + 16 * Sh::kd_unit((HS / 32) * g) + 16 * (s % kMi);
+  };
   auto vaddr = [&](int b) { return vb0 + (16 * b + col) * Sh::kVtRow + 16 * g; };
   bf16x8_t kbuf[kPre], vbuf[kPreV];
   float4 ka[2], ke[2], ks[2];
