@@ -836,12 +836,12 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
     // One pipeline iteration. Tiles whose keys are all visible to every row come first and run without the causal
     // mask; the rest (the chunk's own keys) run with it.
     // With the phase it % 6 known at compile time (the unrolled loop below), every buffer of the iteration sits at a
-    // constant LDS offset, so the ds instructions take it as an immediate instead of per-tile address arithmetic; that
-    // loop also stops 11 tiles before the end, so its iterations skip the end-of-split checks (kSteady).
+    // constant LDS offset, so the ds instructions take it as an immediate instead of per-tile address arithmetic.
+    // Iterations at least 6 tiles before the end of the split (that loop's, and PH = -2) skip the end-of-split checks.
     auto iteration = [&](int it, auto mask_tag, auto phase_tag) {
       constexpr bool kMask = decltype(mask_tag)::value;
-      constexpr int PH = decltype(phase_tag)::value;  // it % 6, or -1 when not known
-      constexpr bool kSteady = PH >= 0;                // it + 5 < ntiles
+      constexpr int PH = decltype(phase_tag)::value;  // it % 6; -1 or -2 (steady) when not known
+      constexpr bool kSteady = PH >= 0 || PH == -2;    // it + 5 < ntiles
       auto pk_at = [&](int k) { return PH >= 0 ? smem + ((PH + k) % 3) * Sh::kPk : pk_of(it + k); };
       auto pk_lds_at = [&](int k) { return PH >= 0 ? lds0 + (uint32_t)(((PH + k) % 3) * Sh::kPk) : pk_lds_of(it + k); };
       auto kd_at = [&](int k) { return PH >= 0 ? smem + Sh::kOffK + ((PH + k) & 1) * Sh::kKd : kd_of(it + k); };
@@ -891,6 +891,10 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
         iteration(it + 5, std::false_type{}, std::integral_constant<int, 5>{});
       }
     }
+    // int8 keys: most tiles take this steady loop (1 % faster there; a second loop body in the int4 kernel, whose
+    // unrolled loop covers these tiles, measured 1 % slower)
+    if constexpr (KFMT != QP_CODES_INT4)
+      for (; it < nplain && it + 6 <= ntiles; ++it) iteration(it, std::false_type{}, std::integral_constant<int, -2>{});
     for (; it < nplain; ++it) iteration(it, std::false_type{}, Unknown{});
     for (; it < ntiles; ++it) iteration(it, std::true_type{}, Unknown{});
     if constexpr (SPAN) wait_vmcnt<0>();
