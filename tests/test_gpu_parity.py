@@ -628,6 +628,25 @@ def test_prefill_key_splits_agree(device, splits):
 
 
 @pytest.mark.parametrize("fmt", ["int4", "int8"])
+@pytest.mark.parametrize("bs,splits", [(16, 1), (16, 2), (32, 1)])
+def test_prefill_loop_boundaries(device, fmt, bs, splits):
+    """Contexts whose 32-key tile counts straddle the kernel's loop boundaries: the six-tile unrolled loop (int4 keys)
+    and the steady loops run only while at least 11 (6) tiles remain, and a split's last tile may hold 1..31 keys; with
+    16-token blocks the run pairs come from a stepping table pointer. 20 query tokens per sequence, so every tile past
+    the chunk is unmasked."""
+    rng = np.random.default_rng(230 + (1 if fmt == "int8" else 0) + 2 * bs + splits)
+    ns = [161, 192, 193, 351, 352, 353, 383, 385, 545, 640, 701]
+    out, emu, ref = _prefill_case(device, rng, fmt, [(20, n) for n in ns], bs=bs, splits=splits)
+    assert np.isfinite(out).all()
+    assert_emulation(out, emu)
+    at = 0
+    for n in ns:
+        sl = slice(at, at + 20)
+        assert O.relerr(out[sl], ref[sl]) < 5e-3, n
+        at += 20
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
 def test_prefill_scores_far_above_the_first_tile(device, fmt):
     """Keys with scales 2^7 .. 2^12 late in the context push scores thousands of log2 units above the first tile's
     maximum: each row raises its maximum where the scores exceed it, scaling its sum and accumulators down in place
