@@ -90,7 +90,8 @@ def decode_bench(torch, args):
 def dropin_bench(torch, args, r):
     """The drop-in path of one layer: unified_attention_int4 on unrotated queries (the query rotation, split-KV
     decode, merge and inverse rotation in one qp_attention call, plus the Python layer's argument checks and
-    ctypes structs), timed eagerly over `steps` calls and as `steps` replays of one captured HIP graph."""
+    ctypes structs), timed eagerly over `steps` calls and as replays of one captured HIP graph of 40 layers (a
+    serving engine captures a whole forward pass; one graph per layer would time the graph launch instead)."""
     from vllm_quantpack.attention import int4_kv, rht
     from vllm_quantpack.tools import synth
     dev = torch.device("cuda:0")
@@ -124,24 +125,23 @@ def dropin_bench(torch, args, r):
         layer(copies[i % n])
     torch.cuda.synchronize()
     eager_us = (time.perf_counter() - t0) * 1e6 / args.steps
-    graphs = []
+    layers = 40
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        for c in copies:
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=side):
-                layer(c)
-            graphs.append(g)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            for i in range(layers):
+                layer(copies[i % n])
     torch.cuda.synchronize()
-    for i in range(args.warmup):
-        graphs[i % n].replay()
+    g.replay()
     torch.cuda.synchronize()
+    replays = max(1, args.steps // layers)
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        graphs[i % n].replay()
+    for _ in range(replays):
+        g.replay()
     torch.cuda.synchronize()
-    graph_us = (time.perf_counter() - t0) * 1e6 / args.steps
+    graph_us = (time.perf_counter() - t0) * 1e6 / (replays * layers)
     del synth, d
     return dict(eager_us=eager_us, graph_us=graph_us)
 
