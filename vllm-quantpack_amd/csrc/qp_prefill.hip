@@ -322,7 +322,7 @@ struct PfRows {
   int row_pos[NT];
 };
 
-// The unpack of one tile cut into stages that pf_step_fast spreads over its MFMA steps (each stage is a few LDS operations
+// The unpack of one tile cut into stages that pf_iter spreads over its MFMA steps (each stage is a few LDS operations
 // and VALU ops, so the MFMA pipe stays busy while they issue). Same results as pf_unpack_k + pf_unpack_v.
 template <int HS, int KFMT>
 struct PfStager {
