@@ -98,17 +98,20 @@ def test_decode_matches_oracle(device, fmt, T):
 @pytest.mark.parametrize("fmt", ["int4", "int8"])
 @pytest.mark.parametrize("T", [1, 4])
 def test_decode_scores_far_above_the_running_maximum(device, fmt, T):
-    """Two key blocks with larger key scales (int4 8x and 20x, int8 2.5x and 5x) give scores 10-60 (log2 units)
-    above the maximum the waves hold when they reach them, so the accumulators are rescaled mid-segment (by assembly
-    on AGPR tiles for the two row tiles of T = 4: 4 tokens x 6 query heads per KV head). The keys before them keep a share of the probability mass (median
-    1-12 %, up to 38 % and more per row), so a rescale that drops or mis-scales them shows against fp64."""
-    rng = np.random.default_rng(400 + T + (10 if fmt == "int8" else 0))
-    f1, f2 = (8.0, 20.0) if fmt == "int4" else (2.5, 5.0)
-    out, emu, ref, _ = _decode_case(device, rng, fmt, [(T, 4000)], segments=7, nq=12, nkv=2,
-                                    big_keys=[(1504, 16, f1), (2900, 8, f2)])
-    assert np.isfinite(out).all()
-    assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
-    assert_emulation(out, emu)
+    """Key blocks with larger key scales. The first two (int4 8x and 20x, int8 2.5x and 5x) give scores 10-60 (log2
+    units) above the maximum the waves hold when they reach them: inside the lazy maximum's 64-unit headroom, so they
+    accumulate with probabilities up to 2^60 while the keys before them keep a share of the probability mass (median
+    1-12 %, up to 38 % and more per row), which a mis-scaled sum or accumulator shows against fp64. A second case adds
+    a third block (int4 256x, int8 64x) up to 250-500 units above, in a chunk that some wave claims after others of its
+    own (chunk 10 of its segment): the accumulators are rescaled mid-segment (by assembly on AGPR tiles for the two
+    row tiles of T = 4: 4 tokens x 6 query heads per KV head)."""
+    f1, f2, f3 = (8.0, 20.0, 256.0) if fmt == "int4" else (2.5, 5.0, 64.0)
+    for big in ([(1504, 16, f1), (2900, 8, f2)], [(1504, 16, f1), (2900, 8, f2), (3790, 8, f3)]):
+        rng = np.random.default_rng(400 + T + (10 if fmt == "int8" else 0))
+        out, emu, ref, _ = _decode_case(device, rng, fmt, [(T, 4000)], segments=7, nq=12, nkv=2, big_keys=big)
+        assert np.isfinite(out).all()
+        assert O.relerr(out, ref) < 5e-3, (len(big), O.relerr(out, ref))
+        assert_emulation(out, emu)
 
 
 @pytest.mark.parametrize("fmt,segments,lens", [("int4", 8, [8192]), ("int4", 5, [8192]), ("int4", 64, [32768]),
