@@ -290,17 +290,20 @@ __device__ __forceinline__ void chunk_reads(const WaveState<HS, KFMT, NCT> &st, 
     }
   }
 
-  // ---- V codes of the lane: channel quad col + 16 b of keys ka, ka + 1 (16-bit pieces), for every block b
+  // ---- V codes of the lane: channel quad col + 16 b of keys ka, ka + 1 (16-bit pieces), for every block b. The
+  // dwords holding the quad are read for both keys at once (rows are 4-byte multiples apart) and one byte permute
+  // keeps the lane's halves (the high ones for odd col).
+  static_assert(VSTR % 4 == 0 && (kKeyBytes + 4) % 4 == 0, "4-byte aligned V codes");
+  const uint32_t vsel = (col & 1) ? 0x07060302u : 0x05040100u;
 #pragma unroll
   for (int b = 0; b < kNb; ++b)
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
       const int ka = (d < 2 ? 4 * g + 2 * d : 16 + 4 * g + 2 * (d - 2));
-      const uint8_t *vr = vb + 2 * (col + 16 * b);
-      u16x2_t pr;
-      pr[0] = *reinterpret_cast<const uint16_t *>(vr + ka * VSTR);
-      pr[1] = *reinterpret_cast<const uint16_t *>(vr + (ka + 1) * VSTR);
-      cr.vx[b][d] = __builtin_bit_cast(uint32_t, pr);
+      const uint8_t *vr = vb + 4 * ((col >> 1) + 8 * b);
+      const uint32_t xa = *reinterpret_cast<const uint32_t *>(vr + ka * VSTR);
+      const uint32_t xb = *reinterpret_cast<const uint32_t *>(vr + (ka + 1) * VSTR);
+      cr.vx[b][d] = __builtin_amdgcn_perm(xb, xa, vsel);
     }
 }
 
