@@ -231,68 +231,45 @@ __device__ __forceinline__ void init_state(WaveState<HS, KFMT, NCT> &st, const D
 
 // ------------------------------------------------------------------------------------- one 32-key chunk
 //
-// A chunk runs in two parts. chunk_reads does everything that reads the chunk's LDS rows: S^T = K Q^T on the MFMAs
-// and the fetch of the lane's V codes into registers (ChunkState). chunk_finish then needs only registers and the
-// per-key scalars, so the LDS rows can be refilled with the next chunk while it runs.
+// A chunk runs in parts. chunk_load reads the lane's V codes (and, with EARLY_K, its K codes of both 16-key
+// sub-tiles) from the chunk's LDS rows into registers (ChunkState); chunk_qk runs S^T = K Q^T on the MFMAs from those
+// codes, or reads each sub-tile's codes from the rows just before its MFMAs (kb given); chunk_finish (softmax, PV)
+// needs only registers and the per-key scalars. Once every read of the rows is done, they can be refilled with the
+// next chunk: with EARLY_K right after chunk_load, before the QK (head 256 and below; at head 512 the codes of both
+// sub-tiles would not fit beside the accumulators, and the refill waits for the QK).
 template <int HS, int NCT>
 struct ChunkState {
   f32x4_t sacc[NCT][2];     // S^T of the two 16-key sub-tiles
   uint32_t vx[HS / 64][4];  // V codes: [channel block b][key pair d], two keys x four channels (nibbles) each
+  uint32_t kc[2][HS / 16];  // K codes of the lane's key for each sub-tile (int4 keys fill the first HS / 32)
 };
 
-// kb/vb: LDS rows of the chunk's 32 keys (key kk at kb + kk * KSTR, vb + kk * VSTR). With QL the query operands
-// are read from LDS (ql: the lane's operand (ct, mi) at ql[(ct * HS / 32 + mi) * 64]) instead of st.qop.
-template <int HS, int KFMT, int NCT, int KSTR, int VSTR, bool QL = false>
-__device__ __forceinline__ void chunk_reads(const WaveState<HS, KFMT, NCT> &st, ChunkState<HS, NCT> &cr,
-                                            const uint8_t *kb, const uint8_t *vb, int col, int g,
-                                            const bf16x8_t *ql = nullptr) {
+// kb/vb: LDS rows of the chunk's 32 keys (key kk at kb + kk * KSTR, vb + kk * VSTR).
+template <int HS, int KFMT, int KSTR>
+__device__ __forceinline__ void load_k_codes(uint32_t (&kc)[HS / 16], const uint8_t *kb, int sub, int col, int g) {
   constexpr int kKeyBytes = KFMT == QP_CODES_INT4 ? HS / 2 : HS;
-  constexpr int kNmi = HS / 32, kNb = HS / 64;
-  f32x4_t (&sacc)[NCT][2] = cr.sacc;
-
-  // ---- S^T = K Q^T, two 16-key sub-tiles
+  constexpr int kDw = kKeyBytes / 16;  // code dwords of the lane per sub-tile
+  const uint8_t *kr = kb + (sub * 16 + col) * KSTR + (kKeyBytes / 4) * g;
 #pragma unroll
-  for (int sub = 0; sub < 2; ++sub) {
-    const uint8_t *kr = kb + (sub * 16 + col) * KSTR + (kKeyBytes / 4) * g;
-    if constexpr (KFMT == QP_CODES_INT4) {
-      uint32_t kd[kNmi];
-#pragma unroll
-      for (int i = 0; i < kNmi; i += 2) {
-        const u32x2_t v2 = *reinterpret_cast<const u32x2_t *>(kr + 4 * i);
-        kd[i] = v2[0];
-        kd[i + 1] = v2[1];
-      }
-#pragma unroll
-      for (int mi = 0; mi < kNmi; ++mi) {
-        const uint32_t x = kd[mi], y = x >> 4;
-        const bf16x8_t kop = as_bf16x8(u32x4_t{nib_pair(x), nib_pair(y), nib_pair(x >> 8), nib_pair(y >> 8)});
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct)
-          sacc[ct][sub] = mfma16x16x32(kop, QL ? ql[(ct * kNmi + mi) * 64] : st.qop[ct][mi],
-                                       mi == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sacc[ct][sub]);
-      }
-    } else {
-#pragma unroll
-      for (int mi = 0; mi < kNmi; ++mi) {
-        const u32x2_t x = *reinterpret_cast<const u32x2_t *>(kr + 8 * mi);
-        u32x4_t y;
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const uint32_t src = x[d >> 1] >> (16 * (d & 1));
-          y[d] = pack_bf16x2((float)(int8_t)(src & 0xFF), (float)(int8_t)(src >> 8));
-        }
-        const bf16x8_t kop = as_bf16x8(y);
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct)
-          sacc[ct][sub] = mfma16x16x32(kop, QL ? ql[(ct * kNmi + mi) * 64] : st.qop[ct][mi],
-                                       mi == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sacc[ct][sub]);
-      }
-    }
+  for (int i = 0; i < kDw; i += 2) {
+    const u32x2_t v2 = *reinterpret_cast<const u32x2_t *>(kr + 4 * i);
+    kc[i] = v2[0];
+    kc[i + 1] = v2[1];
   }
+}
 
-  // ---- V codes of the lane: channel quad col + 16 b of keys ka, ka + 1 (16-bit pieces), for every block b. The
-  // dwords holding the quad are read for both keys at once (rows are 4-byte multiples apart) and one byte permute
-  // keeps the lane's halves (the high ones for odd col).
+template <int HS, int KFMT, int NCT, int KSTR, int VSTR, bool EARLY_K>
+__device__ __forceinline__ void chunk_load(ChunkState<HS, NCT> &cr, const uint8_t *kb, const uint8_t *vb, int col,
+                                           int g) {
+  constexpr int kKeyBytes = KFMT == QP_CODES_INT4 ? HS / 2 : HS;
+  constexpr int kNb = HS / 64;
+  if constexpr (EARLY_K) {
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) load_k_codes<HS, KFMT, KSTR>(cr.kc[sub], kb, sub, col, g);
+  }
+  // V codes of the lane: channel quad col + 16 b of keys ka, ka + 1 (16-bit pieces), for every block b. The dwords
+  // holding the quad are read for both keys at once (rows are 4-byte multiples apart) and one byte permute keeps the
+  // lane's halves (the high ones for odd col).
   static_assert(VSTR % 4 == 0 && (kKeyBytes + 4) % 4 == 0, "4-byte aligned V codes");
   const uint32_t vsel = (col & 1) ? 0x07060302u : 0x05040100u;
 #pragma unroll
@@ -305,6 +282,40 @@ __device__ __forceinline__ void chunk_reads(const WaveState<HS, KFMT, NCT> &st, 
       const uint32_t xb = *reinterpret_cast<const uint32_t *>(vr + (ka + 1) * VSTR);
       cr.vx[b][d] = __builtin_amdgcn_perm(xb, xa, vsel);
     }
+}
+
+// S^T = K Q^T of the two 16-key sub-tiles from the loaded codes. With QL the query operands are read from LDS (ql:
+// the lane's operand (ct, mi) at ql[(ct * HS / 32 + mi) * 64]) instead of st.qop.
+template <int HS, int KFMT, int NCT, int KSTR, bool QL = false>
+__device__ __forceinline__ void chunk_qk(const WaveState<HS, KFMT, NCT> &st, ChunkState<HS, NCT> &cr,
+                                         const uint8_t *kb, int col, int g, const bf16x8_t *ql = nullptr) {
+  constexpr int kNmi = HS / 32;
+  f32x4_t (&sacc)[NCT][2] = cr.sacc;
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    if (kb) load_k_codes<HS, KFMT, KSTR>(cr.kc[sub], kb, sub, col, g);
+#pragma unroll
+    for (int mi = 0; mi < kNmi; ++mi) {
+      bf16x8_t kop;
+      if constexpr (KFMT == QP_CODES_INT4) {
+        const uint32_t x = cr.kc[sub][mi], y = x >> 4;
+        kop = as_bf16x8(u32x4_t{nib_pair(x), nib_pair(y), nib_pair(x >> 8), nib_pair(y >> 8)});
+      } else {
+        const uint32_t x[2] = {cr.kc[sub][2 * mi], cr.kc[sub][2 * mi + 1]};
+        u32x4_t y;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint32_t src = x[d >> 1] >> (16 * (d & 1));
+          y[d] = pack_bf16x2((float)(int8_t)(src & 0xFF), (float)(int8_t)(src >> 8));
+        }
+        kop = as_bf16x8(y);
+      }
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+        sacc[ct][sub] = mfma16x16x32(kop, QL ? ql[(ct * kNmi + mi) * 64] : st.qop[ct][mi],
+                                     mi == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sacc[ct][sub]);
+    }
+  }
 }
 
 // Two row tiles up to head 256 exceed the 256 architectural VGPRs and run one wave per SIMD. Left to the compiler,
@@ -438,13 +449,14 @@ __device__ __forceinline__ void chunk_finish(WaveState<HS, KFMT, NCT> &st, const
   }
 }
 
-// Both parts back to back, for loaders whose LDS rows are not refilled during the chunk.
+// All parts back to back, for loaders whose LDS rows are not refilled during the chunk.
 template <int HS, int KFMT, int NCT, int KSTR, int VSTR>
 __device__ __forceinline__ void compute_chunk(WaveState<HS, KFMT, NCT> &st, const uint8_t *kb, const uint8_t *vb,
                                               const uint8_t *fb, int k0, int kend, int causal_lim, int col, int g,
                                               f32x4_t *rs) {
   ChunkState<HS, NCT> cr;
-  chunk_reads<HS, KFMT, NCT, KSTR, VSTR>(st, cr, kb, vb, col, g);
+  chunk_qk<HS, KFMT, NCT, KSTR>(st, cr, kb, col, g);
+  chunk_load<HS, KFMT, NCT, KSTR, VSTR, false>(cr, kb, vb, col, g);
   chunk_finish<HS, KFMT, NCT>(st, cr, fb, k0, kend, causal_lim, g, rs);
 }
 
@@ -992,13 +1004,14 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
     }
     wave_sync();
     ChunkState<HS, NCT> cr;
-    chunk_reads<HS, KFMT, NCT, Sh::kCell, Sh::kCell, kQL>(st, cr, stage, stage + Sh::kKeyBytes + 4, col, g,
-                                                          qsh + lane);
+    constexpr bool kEarlyK = HS <= 256;
+    if constexpr (!kEarlyK) chunk_qk<HS, KFMT, NCT, Sh::kCell, kQL>(st, cr, stage, col, g, qsh + lane);
+    chunk_load<HS, KFMT, NCT, Sh::kCell, Sh::kCell, kEarlyK>(cr, stage, stage + Sh::kKeyBytes + 4, col, g);
     int nc = 0;
     if (lane == 0) nc = atomicAdd(&next_chunk, 1);
     nc = uniform(nc);
     if (nc < nchunks) {
-      // the stage's K and V codes are in registers now: refill it before the softmax and PV run
+      // the stage's K and V codes are in registers now: refill it before the QK, softmax and PV run
       wait_lgkm0();  // every read of this stage has returned before the DMA may overwrite it
       wave_sync();
       issue_span_dma<Sh>(p, trow, kstart + nc * kChunk, kend, h, lane, stage);
@@ -1006,6 +1019,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
     } else {
       cid[si] = -1;
     }
+    if constexpr (kEarlyK) chunk_qk<HS, KFMT, NCT, Sh::kCell, kQL>(st, cr, nullptr, col, g, qsh + lane);
     chunk_finish<HS, KFMT, NCT>(st, cr, reinterpret_cast<const uint8_t *>(fl), k0, kend, causal_lim, g,
                                 &rsc[w][lane]);
     return true;
