@@ -16,7 +16,7 @@
 //     staging), in one or two stages per wave, waits placed by hand; any other strided layout goes through VGPR
 //     buffer loads into padded LDS rows.
 //   * 8 waves (two per SIMD) for one row tile up to head 256; 4 waves for two row tiles (their O^T accumulators in
-//     AGPRs through inline-assembly MFMAs, the query operands read from LDS) and for head 512, where more than 16
+//     AGPRs through inline-assembly MFMAs, the query operands in VGPRs) and for head 512, where more than 16
 //     rows run as workgroups of whole tokens.
 //   * QK^T runs as S^T = K Q^T on v_mfma_f32_16x16x32_bf16 with the K tile as the A operand: nibbles become exact
 //     bf16 integers 128 + n (one v_bitop3 per pair plus shifts), the Q operand is permuted to match; a caller that
@@ -284,11 +284,10 @@ __device__ __forceinline__ void chunk_load(ChunkState<HS, NCT> &cr, const uint8_
     }
 }
 
-// S^T = K Q^T of the two 16-key sub-tiles from the loaded codes. With QL the query operands are read from LDS (ql:
-// the lane's operand (ct, mi) at ql[(ct * HS / 32 + mi) * 64]) instead of st.qop.
-template <int HS, int KFMT, int NCT, int KSTR, bool QL = false>
+// S^T = K Q^T of the two 16-key sub-tiles from the loaded codes, with the query operands held in registers.
+template <int HS, int KFMT, int NCT, int KSTR>
 __device__ __forceinline__ void chunk_qk(const WaveState<HS, KFMT, NCT> &st, ChunkState<HS, NCT> &cr,
-                                         const uint8_t *kb, int col, int g, const bf16x8_t *ql = nullptr) {
+                                         const uint8_t *kb, int col, int g) {
   constexpr int kNmi = HS / 32;
   f32x4_t (&sacc)[NCT][2] = cr.sacc;
 #pragma unroll
@@ -312,7 +311,7 @@ __device__ __forceinline__ void chunk_qk(const WaveState<HS, KFMT, NCT> &st, Chu
       }
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct)
-        sacc[ct][sub] = mfma16x16x32(kop, QL ? ql[(ct * kNmi + mi) * 64] : st.qop[ct][mi],
+        sacc[ct][sub] = mfma16x16x32(kop, st.qop[ct][mi],
                                      mi == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sacc[ct][sub]);
     }
   }
@@ -930,10 +929,6 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
   constexpr bool kOwnMerge = NCT * 16 * (HS + 4) * 4 <= kStages * 2 * Sh::kHalf;
   __shared__ float mst[2][kOwnMerge ? WAVES * NCT * 16 : 1];
   __shared__ f32x4_t rsc[WAVES][acc_in_agprs<HS, KFMT, NCT>() ? 64 : 1];  // rescale of AGPR accumulators
-  // Two row tiles of query operands (64 registers at head 256) are read from LDS instead of being held: the wave
-  // state then fits the VGPRs without spills. Every wave of the workgroup attends the same rows.
-  constexpr bool kQL = NCT == 2 && HS <= 256;
-  __shared__ bf16x8_t qsh[kQL ? NCT * (HS / 32) * 64 : 1];
   // Rotated query rows (rotate_rows_shared): their own buffer at one row tile; with two the stage cells hold them until
   // every wave has read its operands (one more barrier before the first copies).
   constexpr bool kQrotOwn = NCT == 1;
@@ -968,13 +963,6 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
   // The query rows load first: their wait is on the vm counter, which would otherwise also wait for the copies.
   WaveState<HS, KFMT, NCT> st;
   init_state(st, p, q0, T, n, h, G, col, g, shared_rot ? qrot : nullptr);
-  if constexpr (kQL) {
-    // every wave stores the same operands, and reads back only what its own lanes stored
-#pragma unroll
-    for (int ct = 0; ct < NCT; ++ct)
-#pragma unroll
-      for (int mi = 0; mi < HS / 32; ++mi) qsh[(ct * (HS / 32) + mi) * 64 + lane] = st.qop[ct][mi];
-  }
   if constexpr (!kQrotOwn) {
     if (shared_rot) __syncthreads();  // every wave has read the rotated rows: the stage cells are free again
   }
@@ -1005,7 +993,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
     wave_sync();
     ChunkState<HS, NCT> cr;
     constexpr bool kEarlyK = HS <= 256;
-    if constexpr (!kEarlyK) chunk_qk<HS, KFMT, NCT, Sh::kCell, kQL>(st, cr, stage, col, g, qsh + lane);
+    if constexpr (!kEarlyK) chunk_qk<HS, KFMT, NCT, Sh::kCell>(st, cr, stage, col, g);
     chunk_load<HS, KFMT, NCT, Sh::kCell, Sh::kCell, kEarlyK>(cr, stage, stage + Sh::kKeyBytes + 4, col, g);
     int nc = 0;
     if (lane == 0) nc = atomicAdd(&next_chunk, 1);
@@ -1019,7 +1007,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
     } else {
       cid[si] = -1;
     }
-    if constexpr (kEarlyK) chunk_qk<HS, KFMT, NCT, Sh::kCell, kQL>(st, cr, nullptr, col, g, qsh + lane);
+    if constexpr (kEarlyK) chunk_qk<HS, KFMT, NCT, Sh::kCell>(st, cr, nullptr, col, g);
     chunk_finish<HS, KFMT, NCT>(st, cr, reinterpret_cast<const uint8_t *>(fl), k0, kend, causal_lim, g,
                                 &rsc[w][lane]);
     return true;
