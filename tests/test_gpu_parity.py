@@ -650,6 +650,19 @@ def test_prefill_loop_boundaries(device, fmt, bs, splits):
 
 
 @pytest.mark.parametrize("fmt", ["int4", "int8"])
+@pytest.mark.parametrize("bs", [16, 48])
+def test_prefill_head_128(device, fmt, bs):
+    """Head 128 (GQA 6): 136- and 200-byte cells, so a 16-cell page run is two or three full 64-lane copies plus an
+    8-lane tail, and the copy slots mix runs; 16-token blocks take the stepping table pointer, 48-token blocks the
+    general run arithmetic."""
+    rng = np.random.default_rng(240 + bs + (1 if fmt == "int8" else 0))
+    out, emu, ref = _prefill_case(device, rng, fmt, [(70, 1900), (12, 500), (3, 37)], bs=bs, hs=128)
+    assert np.isfinite(out).all()
+    assert_emulation(out, emu)
+    assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
 def test_prefill_scores_far_above_the_first_tile(device, fmt):
     """Keys with scales 2^7 .. 2^12 late in the context push scores thousands of log2 units above the first tile's
     maximum: each row raises its maximum where the scores exceed it, scaling its sum and accumulators down in place
