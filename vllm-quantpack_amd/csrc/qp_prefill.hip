@@ -110,8 +110,8 @@ __device__ __forceinline__ void pf_runs(const PrefillParams &p, int k0, int kend
 // HBM -> LDS copies of a tile's two 16-cell page runs into its packed slot (run r's unit u at LDS byte pk + 16 (r
 // kRunUnits + u)). The copies are numbered full ones first: q < kFull are run 0's 64-unit copies, then run 1's, then
 // the two runs' partial tails (lanes past the run do not copy); copy q goes to wave q % 4 as its (q / 4)-th. Slot i
-// of all four waves then reads one run whenever copies 4i .. 4i + 3 do (all of them for 16-cell int4 runs at head
-// 256), so that run's base is chosen at compile time. Waves whose last slot is past the plan copy one of the last
+// of all four waves then reads one run whenever copies 4i .. 4i + 3 do (the two slots of full copies for int4 keys
+// at head 256; the third holds the tails), so that run's base is chosen at compile time. Waves whose last slot is past the plan copy one of the last
 // copies again (the same bytes to the same place, complete before the barrier that follows their wait): every wave
 // then issues kMax copies per tile and waits on a count fixed at compile time. A copy reads one run: the run's
 // scalar base plus the lane's fixed offset, so a tile costs the waves two run bases and one M0 per copy, and no
