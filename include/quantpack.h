@@ -203,8 +203,10 @@ typedef struct qp_attention_args {
   int64_t segm_stat_stride[2];
   int32_t segm_rows;
   int32_t num_segments;
-  int32_t max_decode_rows;     /* query rows (tokens x GQA heads) one split-KV workgroup may hold: 16 or 32 (0 = 32);
-                                  above it a sequence's tokens are served in groups that each read the segment */
+  int32_t max_decode_rows;     /* query rows (tokens x GQA heads) one split-KV workgroup may hold in a batch of short
+                                  sequences: 16 or 32 (0 = 32); above it a sequence's tokens are served in groups that
+                                  each read the segment. Mixed batches (short sequences beside prefill chunks, routed
+                                  on the device) always use groups of at most 16 rows */
   const float *rht_signs;      /* optional: rotate q on load and the output back */
   float rht_out_scale;
   void *workspace;             /* >= qp_attention_workspace_size bytes, 256-byte aligned (NULL when that is 0) */

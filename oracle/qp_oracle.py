@@ -10,9 +10,12 @@ vendor; where a detail comes from vLLM and not from the plugin's own text, the d
 Pinning (the checks that tie each function to something other than its own formula) is done in
 tests/test_oracle_pinning.py; the table there names, per function, the known answers, closed forms and planted
 mistakes used. Every function below is pinned by at least one of them. Parity unpinned at bit level, and said so in
-the docstrings concerned: the fused multiply-add assumed in the int4 store's `v * inv + zp` (`_fma32`), vLLM's own
-RHT sign vector (`rht_signs`), and the int4 store's key half (inferred equal to its value half). Those are pinned only
-to tolerance, through the fp64 closed form.
+the docstrings concerned: the fused multiply-add assumed in the int4 store's `v * inv + zp` (`_fma32`), the correctly
+rounded fp32 divisions assumed in the store (`k / k_scale`, `(max - min) / 15`, `-min / scale` and `1 / scale`,
+k8v4_ops.py:35-36,52-54: the text does not say how the compiled Triton store divides, and an approximate division
+would move codes that sit on a rounding boundary), vLLM's own RHT sign vector (`rht_signs`), and the int4 store's key
+half (inferred equal to its value half). Those are pinned only to tolerance, through the fp64 closed form (the
+divisions also by the known answers on rows whose quotients are exact or far from a boundary).
 """
 from __future__ import annotations
 
@@ -441,7 +444,8 @@ def _fma32(a, b, c) -> np.ndarray:
 def quantize_int4(v: np.ndarray):
     """Asymmetric int4 per (token, head) as the value half of `_store_k8v4` (k8v4_ops.py:42-63), which states it
     follows vLLM's int4 store (:22; the int4 store itself is in vLLM: its key half is inferred to be the same).
-    v: [..., hs] fp32 values. Returns (nibble-pair bytes [..., hs/2] uint8, word [...] uint32)."""
+    v: [..., hs] fp32 values. Returns (nibble-pair bytes [..., hs/2] uint8, word [...] uint32). The divisions are taken
+    as correctly rounded fp32 (numpy's), an assumption about the compiled store: parity unpinned there."""
     v = np.asarray(v, np.float32)
     vmin = v.min(axis=-1)
     vmax = v.max(axis=-1)
@@ -456,7 +460,8 @@ def quantize_int4(v: np.ndarray):
 
 def quantize_int8(k: np.ndarray):
     """Key half of `_store_k8v4` (k8v4_ops.py:30-39): scale = max(absmax / 127, 1e-6), codes =
-    clamp(round(k / scale), -127, 127). Returns (int8 codes [..., hs], fp32 scale bits [...] uint32)."""
+    clamp(round(k / scale), -127, 127). Returns (int8 codes [..., hs], fp32 scale bits [...] uint32). The divisions
+    are taken as correctly rounded fp32 (numpy's), an assumption about the compiled store: parity unpinned there."""
     k = np.asarray(k, np.float32)
     scale = np.maximum(np.abs(k).max(axis=-1) / np.float32(127.0), np.float32(1e-6)).astype(np.float32)
     q = np.clip(round_half_away(k / scale[..., None]), -127, 127).astype(np.int8)

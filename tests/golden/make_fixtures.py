@@ -7,7 +7,8 @@ Contents:
           kernel and the fp64 closed form, rounded to fp16), decode_segments;
   prefill: q_prefill (bf16 bits, the last 4 positions), prefill_emu / prefill_ref (fp16);
   unpack: unpack_start, unpack_key / unpack_value (bf16 bits of positions [start, start + 16));
-  store: store_key / store_value (bf16 bits, 4 tokens), store_slots, store_cells (uint8 cells after the store).
+  store: store_key / store_value (bf16 bits, 4 tokens, some rows all zero or constant), store_slots, store_cells
+         (uint8 cells after the store).
 
 The fixture is produced by the oracle only (no reference code runs); tests/test_golden.py checks that the oracle
 still reproduces it exactly and that the HIP kernels meet it.
@@ -54,6 +55,10 @@ def build():
     f["unpack_value"] = O.unpack_segment(v, table, 21, 16, "value")
     sk = O.f32_to_bf16_bits(rng.standard_normal((4, NKV, HS)).astype(np.float32))
     sv = O.f32_to_bf16_bits(rng.standard_normal((4, NKV, HS)).astype(np.float32))
+    # rows without spread (all zero, constant): the store's 1e-6 scale floors set their words and codes
+    for (t, h), c in zip([(0, 1), (2, 2), (3, 3), (2, 0)], [0.0, 0.5, -0.5, 1e-5]):
+        sk[t, h] = O.f32_to_bf16_bits(np.full(HS, c, np.float32))
+        sv[t, (h + 1) % NKV] = O.f32_to_bf16_bits(np.full(HS, c, np.float32))
     slots = np.array([3, -1, 17, 30], np.int64)          # block 0 slot 3, skipped, block 1 slot 1, block 1 slot 14
     fresh = O.new_cache(2, NKV, BS, O.int4_cell_bytes(HS))
     O.store(O.int4_views(fresh, HS), O.bf16_bits_to_f32(sk), O.bf16_bits_to_f32(sv), slots)

@@ -128,95 +128,42 @@ def test_missing_library_fails_loudly(monkeypatch):
 
 
 # --------------------------------------------------------------------------------- reference known answers
+#
+# Sizing and switches of the drop-in, held to the literal values the reference's own tests expect of its functions
+# (tests/test_int4_kv.py:23-87). The vLLM hooks themselves (segment-buffer sizing in the metadata builder, the rebinding
+# of the int4 module) run on the stand-in vLLM of tests/test_vllm_hooks.py.
 
-def test_disabled_by_environment(monkeypatch):
+# (VLLM_QUANTPACK_INT4_DECODE or None, CUs or SMs, expected decode_tiles): the default tile and warps with segments
+# clamp(next_pow2(ceil(units / 4)), 16, 128), and the override's three or four comma-separated values, "auto"
+# standing for the default segment count.
+DECODE_TILES = [
+    (None, 188, (64, 4, 64)), (None, 84, (64, 4, 32)), (None, 36, (64, 4, 16)), (None, 8, (64, 4, 16)),
+    (None, 132, (64, 4, 64)), (None, 512, (64, 4, 128)), (None, 256, (64, 4, 64)),
+    ("32,8,32", 188, (32, 8, 32)), ("64,4,auto", 84, (64, 4, 32)),
+    ("64,4,auto,16", 188, (64, 4, 64, 16)), ("64,4,32,32", 84, (64, 4, 32, 32)),
+]
+
+
+@pytest.mark.parametrize("env,units,want", DECODE_TILES,
+                         ids=[f"{e or 'default'}@{u}" for e, u, _ in DECODE_TILES])
+def test_decode_tiles_known_answers(monkeypatch, env, units, want):
+    from vllm_quantpack.attention import int4_kv
+    if env is None:
+        monkeypatch.delenv("VLLM_QUANTPACK_INT4_DECODE", raising=False)
+    else:
+        monkeypatch.setenv("VLLM_QUANTPACK_INT4_DECODE", env)
+    assert int4_kv.decode_tiles(units) == want
+
+
+def test_patch_is_a_no_op_when_switched_off_or_without_vllm(monkeypatch):
+    """VLLM_QUANTPACK_INT4_KV=0 turns the patch off; a vLLM without the int4 ops module leaves it undone. Either way
+    patch_int4_kv reports False and changes nothing."""
     from vllm_quantpack.attention import int4_kv
     monkeypatch.setenv("VLLM_QUANTPACK_INT4_KV", "0")
     assert int4_kv.patch_int4_kv(LOG) is False
-
-
-def test_vllm_without_int4_mode_leaves_everything(monkeypatch):
-    from vllm_quantpack.attention import int4_kv
+    monkeypatch.delenv("VLLM_QUANTPACK_INT4_KV")
     monkeypatch.setattr(int4_kv, "MODULE", "vllm_quantpack_no_such_module")
     assert int4_kv.patch_int4_kv(LOG) is False
-
-
-def _fake_triton_attn(monkeypatch):
-    mod = types.ModuleType("vllm.v1.attention.backends.triton_attn")
-    mod.NUM_PAR_SOFTMAX_SEGMENTS = 16
-
-    class Builder:
-        def __init__(self, kv_cache_spec, layer_names, vllm_config, device):
-            self.num_par_softmax_segments = mod.NUM_PAR_SOFTMAX_SEGMENTS
-
-    mod.TritonAttentionMetadataBuilder = Builder
-    for name in ("vllm", "vllm.v1", "vllm.v1.attention", "vllm.v1.attention.backends"):
-        monkeypatch.setitem(sys.modules, name, sys.modules.get(name) or types.ModuleType(name))
-    monkeypatch.setitem(sys.modules, mod.__name__, mod)
-    monkeypatch.setattr(sys.modules["vllm.v1.attention.backends"], "triton_attn", mod, raising=False)
-    return mod
-
-
-def _config(dtype):
-    return types.SimpleNamespace(cache_config=types.SimpleNamespace(cache_dtype=dtype))
-
-
-def test_decode_segments_only_for_int4_caches(monkeypatch):
-    from vllm_quantpack.attention import int4_kv
-    mod = _fake_triton_attn(monkeypatch)
-    assert int4_kv._patch_decode_segments(64, LOG) == 64
-    assert mod.TritonAttentionMetadataBuilder(None, [], _config("int4_per_token_head"), None).num_par_softmax_segments == 64
-    assert mod.TritonAttentionMetadataBuilder(None, [], _config("k8v4_per_token_head"), None).num_par_softmax_segments == 64
-    assert mod.TritonAttentionMetadataBuilder(None, [], _config("auto"), None).num_par_softmax_segments == 16
-    assert mod.NUM_PAR_SOFTMAX_SEGMENTS == 16
-
-
-def test_decode_segments_not_power_of_two_left_stock(monkeypatch):
-    from vllm_quantpack.attention import int4_kv
-    mod = _fake_triton_attn(monkeypatch)
-    assert int4_kv._patch_decode_segments(48, LOG) == 0
-    assert mod.TritonAttentionMetadataBuilder(None, [], _config("int4_per_token_head"), None).num_par_softmax_segments == 16
-
-
-def test_patch_installs_hip_functions_into_the_stock_module(monkeypatch):
-    """With a stand-in of vLLM's int4 module, patch_int4_kv rebinds unified_attention_int4 and the store."""
-    from vllm_quantpack import _hip
-    from vllm_quantpack.attention import int4_kv
-    if not os.path.exists(_hip.LIB_PATH):
-        pytest.skip("library not built")
-    stock = types.ModuleType("vllm_quantpack_fake_int4")
-    stock.unified_attention_int4 = lambda *a, **k: "stock"
-    stock.reshape_and_cache_int4 = lambda *a, **k: "stock"
-    monkeypatch.setitem(sys.modules, stock.__name__, stock)
-    monkeypatch.setattr(int4_kv, "MODULE", stock.__name__)
-    assert int4_kv.patch_int4_kv(LOG) is True
-    assert getattr(stock.unified_attention_int4, "_quantpack", False)
-    assert getattr(stock.reshape_and_cache_int4, "_quantpack", False)
-    assert int4_kv.patch_int4_kv(LOG) is True          # idempotent
-
-
-def test_decode_override_from_environment(monkeypatch):
-    from vllm_quantpack.attention import int4_kv
-    monkeypatch.setenv("VLLM_QUANTPACK_INT4_DECODE", "32,8,32")
-    assert int4_kv.decode_tiles(188) == (32, 8, 32)
-    monkeypatch.setenv("VLLM_QUANTPACK_INT4_DECODE", "64,4,auto")
-    assert int4_kv.decode_tiles(84) == (64, 4, 32)
-
-
-def test_decode_override_accepts_query_row_cap(monkeypatch):
-    from vllm_quantpack.attention import int4_kv
-    monkeypatch.setenv("VLLM_QUANTPACK_INT4_DECODE", "64,4,auto,16")
-    assert int4_kv.decode_tiles(188) == (64, 4, 64, 16)
-    monkeypatch.setenv("VLLM_QUANTPACK_INT4_DECODE", "64,4,32,32")
-    assert int4_kv.decode_tiles(84) == (64, 4, 32, 32)
-
-
-@pytest.mark.parametrize("sms,segments", [(188, 64), (84, 32), (36, 16), (8, 16), (132, 64), (512, 128), (256, 64)],
-                         ids=["rtx-pro-6000", "a40", "rtx-5060-ti", "tiny", "h100", "cap", "mi355x"])
-def test_segments_follow_cu_count(monkeypatch, sms, segments):
-    from vllm_quantpack.attention import int4_kv
-    monkeypatch.delenv("VLLM_QUANTPACK_INT4_DECODE", raising=False)
-    assert int4_kv.decode_tiles(sms) == (64, 4, segments)
 
 
 @pytest.mark.parametrize("requested,seqs,heads,sms,want", [(64, 1, 4, 256, 64), (64, 32, 4, 256, 16),

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 from oracle import qp_oracle as O
-from test_oracle_pinning import fma_rows
+from test_oracle_pinning import degenerate_rows, fma_rows
 from qp_testlib import assert_emulation, bf16_tensor, i32, random_cache, run_decode, to_f32, torch_cache
 
 pytestmark = pytest.mark.gpu
@@ -159,12 +159,12 @@ def test_decode_layouts_and_block_sizes(device, layout, bs):
 
 
 @pytest.mark.parametrize("fmt,T", [("int4", 1), ("int4", 2), ("int4", 4), ("int8", 2)])
-def test_decode_span_and_row_loaders_agree(device, fmt, T, monkeypatch):
-    """The HND page-span kernel (HBM -> LDS copies) and the generic strided-row kernel on the same cache."""
-    monkeypatch.delenv("QP_DECODE_ROWS", raising=False)
+def test_decode_span_and_row_loaders_agree(device, fmt, T):
+    """The HND page-span kernel (HBM -> LDS copies) and the generic strided-row kernel on the same cache contents:
+    the same seed fills the same logical cells, stored HND (whole 16-cell page runs, the span kernel) and NHD (slots of
+    one head strided by the KV heads, the strided kernel)."""
     a, emu, ref, _ = _decode_case(device, np.random.default_rng(5), fmt, [(T, 3000), (1, 200)], segments=9)
-    monkeypatch.setenv("QP_DECODE_ROWS", "1")
-    b, _, _, _ = _decode_case(device, np.random.default_rng(5), fmt, [(T, 3000), (1, 200)], segments=9)
+    b, _, _, _ = _decode_case(device, np.random.default_rng(5), fmt, [(T, 3000), (1, 200)], layout="nhd", segments=9)
     assert_emulation(a, emu)
     assert_emulation(b, emu)
     assert O.relerr(a, ref) < 5e-3 and O.relerr(b, ref) < 5e-3
@@ -402,6 +402,11 @@ def test_store_bit_exact(device, fmt, layout):
     val[1:1 + len(rows), 0] = O.f32_to_bf16_bits(rows)
     if fmt == "int4":
         key[1:1 + len(rows), 1] = O.f32_to_bf16_bits(rows)
+    # all-zero and constant rows, where the scale floors of both halves decide the word and the codes
+    flat = degenerate_rows(HS)
+    val[10:10 + len(flat), 2] = O.f32_to_bf16_bits(flat)
+    key[10:10 + len(flat), 3] = O.f32_to_bf16_bits(flat)
+    key[20:20 + len(flat)] = O.f32_to_bf16_bits(flat)[:, None, :]
     slots = rng.permutation(nb * bs)[:n].astype(np.int64)
     slots[::17] = -1
     k8v4_kv.store(None, bf16_tensor(key, device), bf16_tensor(val, device), kc, vc,
@@ -634,7 +639,7 @@ def test_prefill_key_splits_agree(device, splits):
 @pytest.mark.parametrize("bs,splits", [(16, 1), (16, 2), (32, 1)])
 def test_prefill_loop_boundaries(device, fmt, bs, splits):
     """Contexts whose 32-key tile counts straddle the kernel's loop boundaries: the six-tile unrolled loop (int4 keys)
-    and the steady loops run only while at least 11 (6) tiles remain, and a split's last tile may hold 1..31 keys; with
+    and the steady loops run only while at least 12 (7) tiles remain, and a split's last tile may hold 1..31 keys; with
     16-token blocks the run pairs come from a stepping table pointer. 20 query tokens per sequence, so every tile past
     the chunk is unmasked."""
     rng = np.random.default_rng(230 + (1 if fmt == "int8" else 0) + 2 * bs + splits)
@@ -647,6 +652,18 @@ def test_prefill_loop_boundaries(device, fmt, bs, splits):
         sl = slice(at, at + 20)
         assert O.relerr(out[sl], ref[sl]) < 5e-3, n
         at += 20
+
+
+@pytest.mark.parametrize("fmt,n", [("int4", 330), ("int4", 1009), ("int8", 1000), ("int8", 721)])
+def test_prefill_table_row_exactly_as_long_as_the_context(device, fmt, n):
+    """One sequence whose block table holds exactly ceil(n / 16) entries and whose last tile has 1..16 keys: the
+    kernel's table reads ahead of the copies stay inside the row (the CPU walk in test_prefill_table_walk checks the
+    indices; this runs the same shapes)."""
+    rng = np.random.default_rng(250 + n)
+    out, emu, ref = _prefill_case(device, rng, fmt, [(20, n)])
+    assert np.isfinite(out).all()
+    assert_emulation(out, emu)
+    assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
 
 
 @pytest.mark.parametrize("fmt", ["int4", "int8"])
@@ -742,11 +759,10 @@ def test_prefill_wide_gqa_query_slices(device):
     assert O.relerr(out, ref) < 5e-3
 
 
-def test_prefill_span_and_row_loaders_agree(device, monkeypatch):
-    monkeypatch.delenv("QP_PREFILL_ROWS", raising=False)
+def test_prefill_span_and_row_loaders_agree(device):
+    """The page-run copies (HND) and the strided gather (NHD) of the prefill kernel on the same cache contents."""
     a, emu, ref = _prefill_case(device, np.random.default_rng(204), "int8", [(64, 1500), (3, 700)])
-    monkeypatch.setenv("QP_PREFILL_ROWS", "1")
-    b, _, _ = _prefill_case(device, np.random.default_rng(204), "int8", [(64, 1500), (3, 700)])
+    b, _, _ = _prefill_case(device, np.random.default_rng(204), "int8", [(64, 1500), (3, 700)], layout="nhd")
     assert_emulation(a, emu)
     assert_emulation(b, emu)
     assert O.relerr(a, b) < 5e-3

@@ -15,7 +15,8 @@
 | max_row_relerr           | hand-computed rows                                                                          |
 | quantize_int4 (_fma32)   | rows where FMA and mul-then-add round differently: the oracle takes the FMA code (assumed,  |
 |                          | parity unpinned against the reference's Triton store)                                       |
-| quantize_int4/int8/store | reference error bounds (tests/test_k8v4_kv.py:147-156), hand-built rows, slot -1 skipped    |
+| quantize_int4/int8/store | reference error bounds (tests/test_k8v4_kv.py:147-156), hand-built rows, slot -1 skipped,   |
+|                          | the 1e-6 scale floors on all-zero and constant rows (known answers from k8v4_ops.py:35,52) |
 | round_half_away          | known answers incl. fp32 `x + 0.5` rounding                                                 |
 | rht                      | R R^T = hs I, Sylvester entries (-1)^popcount(i & j), pure-Python hash of the signs          |
 | prefill_dequant_attend   | fp64 attention within 1e-2                                                                  |
@@ -352,6 +353,49 @@ def test_quantize_int8_hand_row():
     s = w.view(np.float32)[0]
     assert s == np.float32(np.float32(2.54) / np.float32(127.0))
     assert list(q[0]) == [-127, 0, 64, 127]            # 1.27 / 0.02 = 63.5 -> half away from zero -> 64
+
+
+# Rows with no spread, where the reference's max(., 1e-6) floors set the scale (k8v4_ops.py:35,52): fp32(1e-6) has
+# the bits 0x358637BD, which the int4 word keeps with its low four bits replaced by the zero point (:58). Each row:
+# (value of every channel, int4 code bytes, int4 word, int8 codes, int8 scale bits), derived by hand from the steps
+#   zero row:   scale 1e-6; zp = round(-0 / 1e-6) = 0 (-0.0 >= 0 takes x + 0.5); codes round(0 * 1e6 + 0) = 0;
+#               int8: scale max(0 / 127, 1e-6) = 1e-6, codes 0;
+#   row 0.5:    scale 1e-6; zp = round(-5e5) -> clamp 0; codes round(5e5) -> clamp 15 (bytes 0xFF);
+#               int8: scale 0.5 / 127 (above the floor), codes 127;
+#   row -0.5:   zp = round(5e5) -> clamp 15; codes round(-5e5 + 15) -> clamp 0; int8 codes -127;
+#   row 1e-5:   scale 1e-6; zp = round(-10.01) -> clamp 0; codes round(bf16(1e-5) * 1e6) = round(10.01) = 10 (bytes
+#               0xAA); int8: scale max(1e-5 / 127, 1e-6) = 1e-6, codes round(10.01) = 10.
+FLOOR = 0x358637BD
+DEGENERATE_ROWS = [(0.0, 0x00, FLOOR & ~0xF, 0, FLOOR),
+                   (0.5, 0xFF, FLOOR & ~0xF, 127, None),
+                   (-0.5, 0x00, (FLOOR & ~0xF) | 15, -127, None),
+                   (1.001358e-05, 0xAA, FLOOR & ~0xF, 10, FLOOR)]
+
+
+def degenerate_rows(hs):
+    """[len(DEGENERATE_ROWS), hs] fp32 rows of one repeated bf16 value each."""
+    return np.array([np.full(hs, O.bf16_bits_to_f32(O.f32_to_bf16_bits(np.float32(v)))) for v, *_ in
+                     DEGENERATE_ROWS], np.float32)
+
+
+def test_store_scale_floor_on_rows_without_spread():
+    """The 1e-6 floors of both halves, on all-zero and constant rows (known answers above): a store without them
+    divides by a zero scale and writes a zero scale word."""
+    x = degenerate_rows(16)
+    codes, words = O.quantize_int4(x)
+    for i, (v, byte, word, k8, k8_bits) in enumerate(DEGENERATE_ROWS):
+        assert (codes[i] == byte).all(), v
+        assert int(words[i]) == word, (v, hex(int(words[i])))
+    q, bits = O.quantize_int8(x)
+    for i, (v, byte, word, k8, k8_bits) in enumerate(DEGENERATE_ROWS):
+        assert (q[i] == k8).all(), v
+        want = k8_bits if k8_bits is not None else int(np.float32(abs(np.float32(v)) / np.float32(127.0)).view(np.uint32))
+        assert int(bits[i]) == want, (v, hex(int(bits[i])))
+    # a row whose spread is below the floor: 0 and bf16(1e-6) = 9.98e-7 give codes 0 and round(0.998) = 1
+    tiny = np.zeros((1, 16), np.float32)
+    tiny[0, 15] = O.bf16_bits_to_f32(O.f32_to_bf16_bits(np.float32(1e-6)))
+    c, w = O.quantize_int4(tiny)
+    assert int(w[0]) == FLOOR & ~0xF and list(c[0]) == [0] * 7 + [0x10]
 
 
 def test_store_error_bounds_and_skipped_slots():

@@ -1,0 +1,133 @@
+"""The block-table entries the MFMA prefill kernel reads with 16-token blocks, walked on the CPU.
+
+prefill_kernel (csrc/qp_prefill.hip) reads the table pair of tile t + 5 one iteration ahead of its copies, through a
+pointer that steps two entries per tile. Its steady iterations (the six-phase unrolled loop of int4 keys, the rolled
+steady loop of int8 keys) take the pair's second entry without checking the split's end, which is only valid when that
+tile is followed by another one. This walk restates the kernel's loop structure (its prologue, its three loops and
+the `it + kPfSteadyLead <= ntiles` bound read from the source) and checks, for every context length mod 32 and the
+key-split geometry the kernel uses, that
+
+* every entry read lies inside the sequence's own row (index < ceil(kend / 16)), so a table whose row holds exactly
+  ceil(n / 16) entries is never read past its end;
+* tile t reads the entries of its own blocks: 2t + kb / 16, and the next one only when its second 16-key run starts
+  before the split's end.
+
+A walk with the bound one tile shorter (the kernel's earlier steady condition) reads one entry past the row, which
+the test also checks, so the walk can see the mistake it guards against."""
+import re
+from pathlib import Path
+
+import pytest
+
+SRC = Path(__file__).resolve().parents[1] / "vllm-quantpack_amd" / "csrc" / "qp_prefill.hip"
+TILE = 32        # keys per tile (kPfKeys)
+DECODE_TILE = 32  # split granularity (QP_DECODE_TILE)
+
+
+def steady_lead() -> int:
+    m = re.search(r"constexpr int kPfSteadyLead = (\d+);", SRC.read_text())
+    assert m, "kPfSteadyLead not found in qp_prefill.hip"
+    return int(m.group(1))
+
+
+def walk(n, qlen, t0, bq, split, splits, int4, lead):
+    """Table indices read by one workgroup (query block at local token t0 of a qlen-token chunk whose last token sees
+    n keys; key split `split` of `splits`), as the kernel reads them. Returns (reads, expected) lists of (tile, index)."""
+    ntok = min(bq, qlen - t0)
+    first_pos = n - qlen + t0
+    kend = max(0, min(n, first_pos + ntok))
+    seg = -(-n // (splits * DECODE_TILE)) * DECODE_TILE
+    kb = split * seg
+    ke = min(kend, kb + seg)
+    if splits > 1 and kb >= n:
+        return [], []
+    ntiles = -(-(ke - kb) // TILE) if ke > kb else 0
+    vis_all = first_pos + 1
+    nplain = min(ntiles, max(0, (vis_all - kb) // TILE))
+    tile_key = lambda t: kb + TILE * t
+    reads, state = [], {"tnext": (kb >> 4) + 8, "next_tile": 4}
+
+    def table_ahead(t, steady):
+        assert t == state["next_tile"], "the table pointer steps one tile at a time"
+        state["next_tile"] += 1
+        tn = state["tnext"]
+        off1 = 1 if steady else min(1, (ke - 1 - tile_key(t)) >> 4)
+        reads.append((t, tn))
+        reads.append((t, tn + off1))
+        state["tnext"] += 2
+
+    def iteration(it, steady):
+        if steady or it + 4 < ntiles:
+            if steady or it + 5 < ntiles:
+                table_ahead(it + 5, steady)
+
+    if ntiles == 0:
+        return [], []
+    if ntiles > 4:
+        table_ahead(4, False)
+    it = 0
+    if int4:
+        while it + 6 <= nplain and it + 5 + lead <= ntiles:
+            for k in range(6):
+                iteration(it + k, True)
+            it += 6
+    else:
+        while it < nplain and it + lead <= ntiles:
+            iteration(it, True)
+            it += 1
+    while it < ntiles:
+        iteration(it, False)
+        it += 1
+    expected = []
+    for t in range(4, ntiles):
+        b0 = tile_key(t) >> 4
+        expected += [(t, b0), (t, b0 + 1 if tile_key(t) + 16 < ke else b0)]
+    return reads, expected
+
+
+def shapes():
+    """Chunks of 20 and 64 tokens over contexts of every residue mod 32 around the loops' bounds, one to three key
+    splits."""
+    for base in (160, 320, 480, 992):
+        for r in range(32):
+            n = base + r
+            for qlen in (20, 64):
+                if qlen <= n:
+                    for splits in (1, 2, 3):
+                        yield n, qlen, splits
+
+
+def out_of_row(lead, int4):
+    bad = []
+    for n, qlen, splits in shapes():
+        bq = 32
+        for t0 in range(0, qlen, bq):
+            for split in range(splits):
+                reads, _ = walk(n, qlen, t0, bq, split, splits, int4, lead)
+                row = -(-n // 16)
+                bad += [(n, qlen, splits, t0, split, t, i) for t, i in reads if i >= row]
+    return bad
+
+
+@pytest.mark.parametrize("int4", [True, False], ids=["int4", "int8"])
+def test_every_table_read_stays_in_the_row(int4):
+    assert out_of_row(steady_lead(), int4) == []
+
+
+@pytest.mark.parametrize("int4", [True, False], ids=["int4", "int8"])
+def test_each_tile_reads_its_own_blocks(int4):
+    lead = steady_lead()
+    for n, qlen, splits in shapes():
+        for t0 in range(0, qlen, 32):
+            for split in range(splits):
+                reads, expected = walk(n, qlen, t0, 32, split, splits, int4, lead)
+                assert reads == expected, (n, qlen, splits, t0, split)
+
+
+@pytest.mark.parametrize("int4", [True, False], ids=["int4", "int8"])
+def test_a_bound_one_tile_shorter_reads_past_the_row(int4):
+    """The walk catches the mistake it guards against: steady iterations up to the split's last tile read the entry
+    after a last tile of 1..16 keys."""
+    bad = out_of_row(steady_lead() - 1, int4)
+    assert bad, "the shorter bound should read past the row"
+    assert all((n % 32) in range(1, 17) for n, *_ in bad)

@@ -169,6 +169,22 @@ def test_patch_rebinds_the_int4_module_once(fake_vllm):
     assert "k8v4_per_token_head" not in fake_vllm.triton_attn.TritonAttentionBackend.supported_kv_cache_dtypes
 
 
+@pytest.mark.parametrize("count,installed", [(64, 64), (128, 128), (48, 0), (96, 0)])
+def test_segment_buffers_sized_for_int4_and_k8v4_layers_only(fake_vllm, count, installed):
+    """_patch_decode_segments (int4_kv.py:229-257): a power-of-two count becomes the segment count of the metadata
+    builder for int4 and k8v4 layers, other dtypes keep vLLM's module constant; any other count is refused (0) and
+    the builder stays stock. The module constant itself never changes."""
+    from vllm_quantpack.attention import int4_kv
+    builder = fake_vllm.triton_attn.TritonAttentionMetadataBuilder
+    cfg = lambda d: types.SimpleNamespace(cache_config=types.SimpleNamespace(cache_dtype=d))  # noqa: E731
+    assert int4_kv._patch_decode_segments(count, LOG) == installed
+    for dtype in ("int4_per_token_head", "k8v4_per_token_head", "auto", "fp8_per_token_head"):
+        quantised = dtype in ("int4_per_token_head", "k8v4_per_token_head")
+        want = installed if installed and quantised else 16
+        assert builder(None, [], cfg(dtype), None).num_par_softmax_segments == want, dtype
+    assert fake_vllm.triton_attn.NUM_PAR_SOFTMAX_SEGMENTS == 16
+
+
 @pytest.mark.parametrize("layout", ["hnd", "nhd"])
 def test_backend_hands_out_k8v4_views_and_unit_scales(fake_vllm, layout):
     """A k8v4 layer gets the int8 key / uint8 value views of its byte cache and both scale views at 1.0; a layer of

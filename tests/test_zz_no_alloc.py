@@ -99,4 +99,9 @@ def test_noalloc_rejects_a_batch_beyond_its_buffer():
     assert "static buffer" in lib.qp_last_error().decode()
     args.max_query_len = 8                                  # a prefill chunk is not for this entry point
     assert lib.qp_attention_noalloc(ctypes.byref(cache), ctypes.byref(args), None) == _hip.QP_ERR_UNSUPPORTED
+    # head 512 with 24 query heads on one KV head: a decode shape qp_attention sends to its prefill path
+    cache.num_kv_heads, cache.head_size = 1, 512
+    args.num_seqs, args.num_tokens, args.max_query_len, args.num_segments = 1, 1, 1, 4
+    assert lib.qp_attention_noalloc(ctypes.byref(cache), ctypes.byref(args), None) == _hip.QP_ERR_UNSUPPORTED
+    assert "head 512" in lib.qp_last_error().decode()
     del torch

@@ -204,6 +204,8 @@ extern "C" int qp_attention(const qp_paged_cache *cache, const qp_attention_args
   if (st != QP_OK) return st;
   st = prefill_run(cache, &P.prefill, route_row, s);
   if (st != QP_OK) return st;
+  // mixed batches: groups of at most 16 rows (one row tile) whatever max_decode_rows says, as the host does not know
+  // each short sequence's query count here
   st = decode_routed(cache, &P.decode, route_row, 16, s);
   if (st != QP_OK) return st;
   qp_merge_args m = {};
@@ -275,6 +277,7 @@ extern "C" int qp_attention_noalloc(const qp_paged_cache *cache, const qp_attent
                "qp_attention_noalloc: only batches of sequences with 1..4 query tokens and at most 32 query rows per "
                "KV head (a decode step)");
   QP_SUPPORTED(hs == 128 || hs == 256 || hs == 512, "qp_attention_noalloc: head size must be 128, 256 or 512");
+  QP_SUPPORTED(hs != 512 || G <= 16, "qp_attention_noalloc: head 512 takes at most 16 query heads per KV head");
   QP_REQUIRE(args->num_segments >= 1 && args->num_segments <= 2048, "qp_attention_noalloc: 1..2048 segments");
   // [segment rows: tokens x heads x segments x head_size | maxima | sums], fp32, each part 256-byte aligned
   const int64_t triples = (int64_t)args->num_tokens * args->num_q_heads * args->num_segments;
@@ -303,6 +306,6 @@ extern "C" int qp_attention_noalloc(const qp_paged_cache *cache, const qp_attent
   a.workspace = nullptr;
   a.workspace_bytes = 0;
   // a batch of short sequences whose rows all fit: qp_attention's decode + merge, which needs no workspace
-  QP_REQUIRE(qp_attention_workspace_size(cache, &a) == 0, "qp_attention_noalloc: not a batch of short sequences");
+  QP_SUPPORTED(qp_attention_workspace_size(cache, &a) == 0, "qp_attention_noalloc: not a batch of short sequences");
   return qp_attention(cache, &a, stream);
 }

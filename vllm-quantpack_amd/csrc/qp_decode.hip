@@ -29,7 +29,8 @@
 //     (128 + zp_k) * sum(q); the output subtracts sum(P_v16 * (16 + zp_v)), accumulated from the same rounded P_v16
 //     that feeds the MFMA. The small value offset keeps the fp32 cancellation of acc - sum P_v16 (16 + zp_v) small
 //     even where most values sit at their zero point.
-//   * Online softmax in base 2 with a lazy rescale (only when a row maximum grows by more than 2^8); the waves'
+//   * Online softmax in base 2 with a lazy rescale (only when a score exceeds the row's running maximum by more than
+//     kLazyRescale = 64 log2 units); the waves'
 //     states merge in LDS at the end (each wave parking its rows in its own stage buffers where they fit) and the
 //     workgroup writes one (acc, m, l) partial per row.
 #include "qp_common.h"
@@ -1723,7 +1724,7 @@ namespace {
 
 int dispatch_hs(const qp_paged_cache *cache, const DecodeParams &p, int nct, dim3 grid, hipStream_t s) {
   const int hs = cache->head_size;
-  const bool span = is_span_layout(cache) && !getenv("QP_DECODE_ROWS");
+  const bool span = is_span_layout(cache);
   QP_SUPPORTED(span || hs != 512 || cache->key.format == QP_CODES_INT4,
                "head 512 with int8 keys needs the standard cell layout");
   if (hs == 512) return dispatch_decode<512>(p, cache->key.format, nct, grid, span, s);

@@ -69,6 +69,10 @@ struct PrefillParams {
 constexpr int kPfKeys = 32;  // keys per tile
 constexpr int kPfWaves = 4;
 constexpr float kPfRescale = 64.f;  // log2 headroom before the running maximum is raised
+// A steady iteration it (no end-of-split checks) needs it + kPfSteadyLead <= ntiles: tile it + 5, whose table entries
+// it reads, is then followed by tile it + 6, so both of its 16-key runs lie before the split's end and both entries
+// exist in the sequence's block-table row.
+constexpr int kPfSteadyLead = 7;
 
 template <int HS, int KFMT>
 struct PfShape {
@@ -811,7 +815,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
       if constexpr (BS16) {
         ahead.bid0 = tnext[0];
         // the second run only if it starts before ke (a byte offset of 0 or 4: the load takes it as its SGPR offset);
-        // a steady iteration's tile is followed by others, so its second run always does
+        // in a steady iteration tile t is followed by another tile (kPfSteadyLead), so its second run always does
         const uint32_t off1 =
             decltype(steady_tag)::value ? 4u : (uint32_t)min(4, ((ke - 1 - tile_key(t)) >> 4) << 2);
         ahead.bid1 = *(const __attribute__((address_space(4))) int32_t *)((const __attribute__((address_space(4))) uint8_t *)tnext + off1);
@@ -837,11 +841,12 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
     // mask; the rest (the chunk's own keys) run with it.
     // With the phase it % 6 known at compile time (the unrolled loop below), every buffer of the iteration sits at a
     // constant LDS offset, so the ds instructions take it as an immediate instead of per-tile address arithmetic.
-    // Iterations at least 6 tiles before the end of the split (that loop's, and PH = -2) skip the end-of-split checks.
+    // Iterations at least kPfSteadyLead tiles before the end of the split (that loop's, and PH = -2) skip the
+    // end-of-split checks.
     auto iteration = [&](int it, auto mask_tag, auto phase_tag) {
       constexpr bool kMask = decltype(mask_tag)::value;
       constexpr int PH = decltype(phase_tag)::value;  // it % 6; -1 or -2 (steady) when not known
-      constexpr bool kSteady = PH >= 0 || PH == -2;    // it + 5 < ntiles
+      constexpr bool kSteady = PH >= 0 || PH == -2;    // it + kPfSteadyLead <= ntiles
       auto pk_at = [&](int k) { return PH >= 0 ? smem + ((PH + k) % 3) * Sh::kPk : pk_of(it + k); };
       auto pk_lds_at = [&](int k) { return PH >= 0 ? lds0 + (uint32_t)(((PH + k) % 3) * Sh::kPk) : pk_lds_of(it + k); };
       auto kd_at = [&](int k) { return PH >= 0 ? smem + Sh::kOffK + ((PH + k) & 1) * Sh::kKd : kd_of(it + k); };
@@ -882,7 +887,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
     // int4 keys only: with int8 keys the unrolled loop's extra live addresses spill 160 bytes per lane and measured
     // 2 % slower (4.47 against 4.37 ms), while int4 keys gain 5 % (3.75 against 3.93 ms)
     if constexpr (SPAN && KFMT == QP_CODES_INT4) {
-      for (; it + 6 <= nplain && it + 11 <= ntiles; it += 6) {  // iterations it .. it + 5 are steady
+      for (; it + 6 <= nplain && it + 5 + kPfSteadyLead <= ntiles; it += 6) {  // iterations it .. it + 5 are steady
         iteration(it, std::false_type{}, std::integral_constant<int, 0>{});
         iteration(it + 1, std::false_type{}, std::integral_constant<int, 1>{});
         iteration(it + 2, std::false_type{}, std::integral_constant<int, 2>{});
@@ -894,7 +899,8 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
     // int8 keys: most tiles take this steady loop (1 % faster there; a second loop body in the int4 kernel, whose
     // unrolled loop covers these tiles, measured 1 % slower)
     if constexpr (KFMT != QP_CODES_INT4)
-      for (; it < nplain && it + 6 <= ntiles; ++it) iteration(it, std::false_type{}, std::integral_constant<int, -2>{});
+      for (; it < nplain && it + kPfSteadyLead <= ntiles; ++it)
+        iteration(it, std::false_type{}, std::integral_constant<int, -2>{});
     for (; it < nplain; ++it) iteration(it, std::false_type{}, Unknown{});
     for (; it < ntiles; ++it) iteration(it, std::true_type{}, Unknown{});
     if constexpr (SPAN) wait_vmcnt<0>();
@@ -1111,7 +1117,7 @@ int prefill_run(const qp_paged_cache *cache, const qp_prefill_args *a, const int
   // sequence s owns query blocks [cu_q[s] / BQ + s, cu_q[s + 1] / BQ + s + 1): an upper bound known on the host
   const unsigned blocks = (unsigned)(a->num_tokens / bq + a->num_seqs);
   const dim3 grid(blocks, cache->num_kv_heads, splits);
-  const bool span = is_span_layout(cache) && cache->key.code_stride[0] < (int64_t(1) << 31) && !getenv("QP_PREFILL_ROWS");
+  const bool span = is_span_layout(cache) && cache->key.code_stride[0] < (int64_t(1) << 31);
   if (hs == 256) {
     if (cache->key.format == QP_CODES_INT4) dispatch_nt<256, QP_CODES_INT4>(p, nt, grid, span, s);
     else dispatch_nt<256, QP_CODES_INT8>(p, nt, grid, span, s);

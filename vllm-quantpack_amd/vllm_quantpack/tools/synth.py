@@ -8,6 +8,8 @@ Workloads (24 query / 4 KV heads, head 256, block 16 unless stated):
   decode-k8v4-ragged-b32   32 requests of 1 or 2 query tokens, contexts lognormal(ln 16384, 1) clipped to
                            [2048, 65536], int8 keys, queries rotated into the Hadamard domain
   prefill-k8v4-128k-c1024  the prefill chunk workload over a k8v4 cache (int8 keys stored by the store as well)
+  prefill-int4-h512-128k-c1024  the prefill chunk workload at head 512 with 16 query / 2 KV heads (the shape of a
+                           Gemma-style global attention layer)
 
 int4 cells: nibbles uniform 0..15; per (token, KV head) fp32 scale ~ lognormal(-3, 0.5) with its low 4 mantissa bits
 replaced by the zero point round(U(6, 9)). k8v4 keys: int8 uniform -127..127, fp32 scale ~ lognormal(-4, 0.5).
@@ -22,7 +24,7 @@ import numpy as np
 NQ, NKV, HS, BS = 24, 4, 256, 16
 
 WORKLOADS = ("decode-int4-4k-t1", "decode-int4-128k-t2", "decode-int4-256k-t4", "prefill-int4-128k-c1024",
-             "decode-k8v4-ragged-b32", "prefill-k8v4-128k-c1024")
+             "decode-k8v4-ragged-b32", "prefill-k8v4-128k-c1024", "prefill-int4-h512-128k-c1024")
 
 
 @dataclass
@@ -121,21 +123,22 @@ def make(name: str, *, small: bool = False) -> Workload:
         return _single(name, rng, 131072 // div, 2)
     if name == "decode-int4-256k-t4":
         return _single(name, rng, 262144 // div, 4)
-    if name in ("prefill-int4-128k-c1024", "prefill-k8v4-128k-c1024"):
+    if name in ("prefill-int4-128k-c1024", "prefill-k8v4-128k-c1024", "prefill-int4-h512-128k-c1024"):
         k8v4 = name.startswith("prefill-k8v4")
+        nq, nkv, hs = (16, 2, 512) if "-h512-" in name else (NQ, NKV, HS)
         cached, chunk = 131072 // div, 1024 // (4 if small else 1)
         n = cached + chunk
         nb = -(-n // BS)
-        kv = fill_k8v4_cache(rng, nb) if k8v4 else fill_int4_cache(rng, nb)
+        kv = fill_k8v4_cache(rng, nb, nkv, BS, hs) if k8v4 else fill_int4_cache(rng, nb, nkv, BS, hs)
         table = rng.permutation(nb).astype(np.int32)
-        q = bf16_bits(rng.standard_normal((chunk, NQ, HS)).astype(np.float32))
-        nk = bf16_bits(rng.standard_normal((chunk, NKV, HS)).astype(np.float32))
-        nv = bf16_bits(rng.standard_normal((chunk, NKV, HS)).astype(np.float32))
+        q = bf16_bits(rng.standard_normal((chunk, nq, hs)).astype(np.float32))
+        nk = bf16_bits(rng.standard_normal((chunk, nkv, hs)).astype(np.float32))
+        nv = bf16_bits(rng.standard_normal((chunk, nkv, hs)).astype(np.float32))
         pos = np.arange(cached, n)
         slots = (table[pos // BS].astype(np.int64) * BS + pos % BS)
         return Workload(name, kv, "int8" if k8v4 else "int4", q, np.array([0, chunk], np.int32),
-                        np.array([n], np.int32), table[None, :], 1.0 / 16, new_key=nk, new_value=nv, new_slots=slots,
-                        meta={"cached": cached})
+                        np.array([n], np.int32), table[None, :], hs ** -0.5, head_size=hs, num_q_heads=nq,
+                        num_kv_heads=nkv, new_key=nk, new_value=nv, new_slots=slots, meta={"cached": cached})
     if name == "decode-k8v4-ragged-b32":
         seqs = 32
         T = rng.integers(1, 3, size=seqs)
