@@ -70,20 +70,25 @@ def decode_bench(torch, args):
         plans[i % n].run()
     torch.cuda.synchronize()
     step_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    # decode-kernel duration: `steps` decode launches queued behind a spin that holds the stream, bracketed by one
-    # pair of events on that stream, so the average is the kernel's execution time in a full queue (an event pair
-    # around every launch would add its own dispatch overhead, about 3 us, to each)
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda._sleep(SPIN_CYCLES)
-    a.record(stream)
-    for i in range(args.steps):
-        plans[i % n].decode()
-    b.record(stream)
-    torch.cuda.synchronize()
-    kern_ms = a.elapsed_time(b) / args.steps
+    # kernel durations: `steps` launches queued behind a spin that holds the stream, bracketed by one pair of events
+    # on that stream, so the average is the execution time in a full queue (an event pair around every launch would
+    # add its own dispatch overhead, about 3 us, to each): the split-KV decode kernel alone (the roofline's kernel)
+    # and the step's two launches (decode + merge).
+    def queued(fn):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(SPIN_CYCLES)
+        a.record(stream)
+        for i in range(args.steps):
+            fn(plans[i % n])
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / args.steps
+
+    kern_ms = queued(lambda pl: pl.decode())
+    pair_ms = queued(lambda pl: (pl.decode(), pl.merge()))
     nbytes = synth.cache_bytes(w)
     result = dict(tokens_per_step=T, step_ms=step_ms, decode_kernel_us=kern_ms * 1e3, bytes=nbytes, segments=S,
-                  out=out, w=w, copies=copies)
+                  pair_us=pair_ms * 1e3, out=out, w=w, copies=copies)
     return result
 
 
@@ -282,8 +287,8 @@ def main(argv=None):
     r = decode_bench(torch, args)
     step_s = r["step_ms"] * 1e-3
     kern_s = r["decode_kernel_us"] * 1e-6
-    log(f"decode: {r['step_ms'] * 1e3:.1f} us/step, decode kernel {r['decode_kernel_us']:.1f} us, "
-        f"{r['bytes'] / kern_s / 1e9:.0f} GB/s")
+    log(f"decode: {r['step_ms'] * 1e3:.1f} us/step, decode kernel {r['decode_kernel_us']:.1f} us "
+        f"({r['bytes'] / kern_s / 1e9:.0f} GB/s), decode + merge queued {r['pair_us']:.1f} us")
     line = {
         "metric": METRIC,
         "value": round(r["tokens_per_step"] / step_s, 1),
@@ -309,6 +314,7 @@ def main(argv=None):
                      "committed summary profiles/decode_span_kernel_decode-int4-128k-t2_traffic.txt (not this run)",
                      "kernel": DECODE_KERNEL,
                      "bytes_per_launch": r["bytes"], "avg_us": round(r["decode_kernel_us"], 2)},
+        "decode_plus_merge_queued_us": round(r["pair_us"], 2),
     }
     if not args.no_prefill:
         try:

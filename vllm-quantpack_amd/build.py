@@ -170,15 +170,17 @@ def _check_inline_mfma(src, verbose):
         raise RuntimeError(f"{src}: spill code in MFMA blocks:\n{lines}")
 
 
-def build(jobs=None, verbose=False):
-    """Compile every csrc/*.hip, check the inline-MFMA wait states and link the shared library. Returns the library
-    path."""
+def build(jobs=None, verbose=False, only=None):
+    """Compile every csrc/*.hip (or only the named ones, reusing the other objects of an earlier build), check the
+    inline-MFMA wait states and link the shared library. Returns the library path."""
     os.makedirs(OBJ, exist_ok=True)
     srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+    todo = [s for s in srcs if not only or os.path.basename(s) in only]
     jobs = jobs or min(8, os.cpu_count() or 1, len(srcs))
     with cf.ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose), srcs))
-        list(ex.map(lambda s: _check_inline_mfma(s, verbose), srcs))
+        list(ex.map(lambda s: _compile(s, verbose), todo))
+        list(ex.map(lambda s: _check_inline_mfma(s, verbose), todo))
+    objs = [os.path.join(OBJ, os.path.basename(s).replace(".hip", ".o")) for s in srcs]
     tmp = LIB + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     if verbose:
@@ -194,8 +196,9 @@ def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--only", default="", help="comma-separated sources to recompile (the rest from _build/)")
     a = ap.parse_args(argv)
-    print(build(a.jobs, a.verbose))
+    print(build(a.jobs, a.verbose, [x for x in a.only.split(",") if x]))
 
 
 if __name__ == "__main__":
