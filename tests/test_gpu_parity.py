@@ -751,12 +751,79 @@ def test_prefill_head_512_query_slices(device, fmt):
     assert O.relerr(out, ref) < 5e-3
 
 
-def test_prefill_wide_gqa_query_slices(device):
-    """16 query heads per KV head is past the MFMA prefill kernel's 12 and takes the slice path as well."""
+def test_prefill_wide_gqa(device):
+    """16 query heads per KV head is past the 16-row-tile kernel's 12: the wide kernel (32x32x16 MFMAs, rows as
+    (token, head) pairs) serves it."""
     rng = np.random.default_rng(405)
     out, emu, ref = _prefill_case(device, rng, "int4", [(20, 1500), (3, 200)], nq=16, nkv=1, hs=128)
     assert_emulation(out, emu)
     assert O.relerr(out, ref) < 5e-3
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+@pytest.mark.parametrize("hs,splits", [(256, 1), (256, 3), (128, 1), (128, 2)])
+def test_prefill_wide_kernel_batches(device, fmt, hs, splits):
+    """The wide kernel on a batch whose row blocks (128 rows at head 256, 256 at head 128) straddle tokens and end
+    mid-block: a long chunk, a first chunk (context == chunk), a single token, a 130-token chunk; 32 query heads on 2
+    KV heads; with key splits, some of them empty."""
+    rng = np.random.default_rng(260 + hs + splits + (1 if fmt == "int8" else 0))
+    lens = [(40, 3000), (7, 7), (1, 500), (130, 900)]
+    out, emu, ref = _prefill_case(device, rng, fmt, lens, nq=32, nkv=2, hs=hs, splits=splits)
+    assert np.isfinite(out).all()
+    assert_emulation(out, emu)
+    assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
+
+
+@pytest.mark.parametrize("fmt,n", [("int4", 330), ("int8", 1000)])
+def test_prefill_wide_table_row_exactly_as_long_as_the_context(device, fmt, n):
+    """One sequence whose block table holds exactly ceil(n / 16) entries and whose last tile has 1..16 keys, on the
+    wide kernel (the CPU walk in test_prefill_table_walk checks its table reads)."""
+    rng = np.random.default_rng(270 + n)
+    out, emu, ref = _prefill_case(device, rng, fmt, [(20, n)], nq=16, nkv=1)
+    assert_emulation(out, emu)
+    assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+def test_prefill_wide_scores_far_above_the_first_tile(device, fmt):
+    """Key scales of 2^7 .. 2^12 late in the context put scores thousands of log2 units above the first tile's
+    maximum, past the wide kernel's headroom: the workgroup runs its split again with the raised maxima (once per
+    jump), and the result still matches."""
+    rng = np.random.default_rng(280 + (1 if fmt == "int8" else 0))
+    big = [(700, 2.0 ** 7), (1300, 2.0 ** 9), (1901, 2.0 ** 12)]
+    out, emu, ref = _prefill_case(device, rng, fmt, [(40, 2000), (9, 1400)], nq=16, nkv=1, splits=1, big_keys=big)
+    assert np.isfinite(out).all()
+    assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
+
+
+def test_prefill_wide_fused_rotations(device):
+    """On the wide kernel: the query rotated on load gives the bits of rotating it first, and the output rotated back
+    in the epilogue (one split) or by the merge (three) matches a separate inverse rotation."""
+    import torch
+
+    from vllm_quantpack.attention import int4_prefill, rht
+    rng = np.random.default_rng(290)
+    n, qlen, bs, nq, nkv = 2500, 50, 16, 32, 2
+    nb = -(-n // bs)
+    kv, _ = random_cache(rng, nb, nkv, bs, HS)
+    _, (kc, vc, ks, vs) = torch_cache(kv, HS, "int4", device)
+    q = bf16_tensor(O.f32_to_bf16_bits(rng.standard_normal((qlen, nq, HS)).astype(np.float32)), device)
+    table = torch.arange(nb, dtype=torch.int32, device=device)[None]
+    signs = rht.signs(HS, device)
+    kw = dict(cu_seqlens_q=i32([0, qlen], device), seqused_k=i32([n], device), block_table=table, max_seqlen_q=qlen,
+              softmax_scale=0.004)
+    a, b = torch.empty_like(q), torch.empty_like(q)
+    int4_prefill.prefill_attention(rht.single_rht(q), kc, vc, ks, vs, a, **kw, num_splits=1)
+    int4_prefill.prefill_attention(q, kc, vc, ks, vs, b, **kw, num_splits=1, query_signs=signs)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    want = O.rht(to_f32(a).astype(np.float64), inverse=True) / HS
+    for splits in (1, 3):
+        got = torch.empty_like(q)
+        int4_prefill.prefill_attention(q, kc, vc, ks, vs, got, **kw, num_splits=splits, query_signs=signs,
+                                       rht_signs=signs, rht_out_scale=1 / HS)
+        torch.cuda.synchronize()
+        assert O.relerr(to_f32(got), want) < 1e-2, splits
 
 
 def test_prefill_span_and_row_loaders_agree(device):

@@ -1,11 +1,11 @@
-"""The block-table entries the MFMA prefill kernel reads with 16-token blocks, walked on the CPU.
+"""The block-table entries the MFMA prefill kernels read with 16-token blocks, walked on the CPU.
 
-prefill_kernel (csrc/qp_prefill.hip) reads the table pair of tile t + 5 one iteration ahead of its copies, through a
-pointer that steps two entries per tile. Its steady iterations (the six-phase unrolled loop of int4 keys, the rolled
-steady loop of int8 keys) take the pair's second entry without checking the split's end, which is only valid when that
-tile is followed by another one. This walk restates the kernel's loop structure (its prologue, its three loops and
-the `it + kPfSteadyLead <= ntiles` bound read from the source) and checks, for every context length mod 32 and the
-key-split geometry the kernel uses, that
+prefill_kernel (csrc/qp_prefill.hip) and prefill_wide_kernel (csrc/qp_prefill_wide.hip) read the table pair of tile
+t + 5 one iteration ahead of its copies, through a pointer that steps two entries per tile. Their steady iterations
+(the tile kernel's six-phase unrolled loop of int4 keys and rolled steady loop of int8 keys, the wide kernel's steady
+loop) take the pair's second entry without checking the split's end, which is only valid when that tile is followed by
+another one. This walk restates each kernel's loop structure (prologue and loops, with the `kPfSteadyLead` bound read
+from the source) and checks, for every context length mod 32 and the key-split geometry the kernels use, that
 
 * every entry read lies inside the sequence's own row (index < ceil(kend / 16)), so a table whose row holds exactly
   ceil(n / 16) entries is never read past its end;
@@ -19,20 +19,24 @@ from pathlib import Path
 
 import pytest
 
-SRC = Path(__file__).resolve().parents[1] / "vllm-quantpack_amd" / "csrc" / "qp_prefill.hip"
+CSRC = Path(__file__).resolve().parents[1] / "vllm-quantpack_amd" / "csrc"
 TILE = 32        # keys per tile (kPfKeys)
 DECODE_TILE = 32  # split granularity (QP_DECODE_TILE)
 
 
 def steady_lead() -> int:
-    m = re.search(r"constexpr int kPfSteadyLead = (\d+);", SRC.read_text())
-    assert m, "kPfSteadyLead not found in qp_prefill.hip"
+    m = re.search(r"constexpr int kPfSteadyLead = (\d+);", (CSRC / "qp_prefill.h").read_text())
+    assert m, "kPfSteadyLead not found in qp_prefill.h"
+    # both kernels bound their steady loops by it (the tile kernel's unrolled loop by it + 5 + kPfSteadyLead)
+    assert "it + 5 + kPfSteadyLead <= ntiles" in (CSRC / "qp_prefill.hip").read_text()
+    assert "it + kPfSteadyLead <= ntiles" in (CSRC / "qp_prefill_wide.hip").read_text()
     return int(m.group(1))
 
 
-def walk(n, qlen, t0, bq, split, splits, int4, lead):
+def walk(n, qlen, t0, bq, split, splits, int4, lead, wide=False):
     """Table indices read by one workgroup (query block at local token t0 of a qlen-token chunk whose last token sees
-    n keys; key split `split` of `splits`), as the kernel reads them. Returns (reads, expected) lists of (tile, index)."""
+    n keys; key split `split` of `splits`), as the kernel reads them (wide: prefill_wide_kernel's loops, whose
+    iterations run up to the split's second-to-last tile). Returns (reads, expected) lists of (tile, index)."""
     ntok = min(bq, qlen - t0)
     first_pos = n - qlen + t0
     kend = max(0, min(n, first_pos + ntok))
@@ -66,18 +70,26 @@ def walk(n, qlen, t0, bq, split, splits, int4, lead):
     if ntiles > 4:
         table_ahead(4, False)
     it = 0
-    if int4:
-        while it + 6 <= nplain and it + 5 + lead <= ntiles:
-            for k in range(6):
-                iteration(it + k, True)
-            it += 6
-    else:
-        while it < nplain and it + lead <= ntiles:
+    if wide:
+        while it + 1 < nplain and it + lead <= ntiles:
             iteration(it, True)
             it += 1
-    while it < ntiles:
-        iteration(it, False)
-        it += 1
+        while it + 1 < ntiles:
+            iteration(it, False)
+            it += 1
+    else:
+        if int4:
+            while it + 6 <= nplain and it + 5 + lead <= ntiles:
+                for k in range(6):
+                    iteration(it + k, True)
+                it += 6
+        else:
+            while it < nplain and it + lead <= ntiles:
+                iteration(it, True)
+                it += 1
+        while it < ntiles:
+            iteration(it, False)
+            it += 1
     expected = []
     for t in range(4, ntiles):
         b0 = tile_key(t) >> 4
@@ -97,37 +109,41 @@ def shapes():
                         yield n, qlen, splits
 
 
-def out_of_row(lead, int4):
+KERNELS = [dict(int4=True), dict(int4=False), dict(int4=True, wide=True)]
+IDS = ["tiles-int4", "tiles-int8", "wide"]
+
+
+def out_of_row(lead, int4, wide=False):
     bad = []
     for n, qlen, splits in shapes():
         bq = 32
         for t0 in range(0, qlen, bq):
             for split in range(splits):
-                reads, _ = walk(n, qlen, t0, bq, split, splits, int4, lead)
+                reads, _ = walk(n, qlen, t0, bq, split, splits, int4, lead, wide)
                 row = -(-n // 16)
                 bad += [(n, qlen, splits, t0, split, t, i) for t, i in reads if i >= row]
     return bad
 
 
-@pytest.mark.parametrize("int4", [True, False], ids=["int4", "int8"])
-def test_every_table_read_stays_in_the_row(int4):
-    assert out_of_row(steady_lead(), int4) == []
+@pytest.mark.parametrize("kernel", KERNELS, ids=IDS)
+def test_every_table_read_stays_in_the_row(kernel):
+    assert out_of_row(steady_lead(), **kernel) == []
 
 
-@pytest.mark.parametrize("int4", [True, False], ids=["int4", "int8"])
-def test_each_tile_reads_its_own_blocks(int4):
+@pytest.mark.parametrize("kernel", KERNELS, ids=IDS)
+def test_each_tile_reads_its_own_blocks(kernel):
     lead = steady_lead()
     for n, qlen, splits in shapes():
         for t0 in range(0, qlen, 32):
             for split in range(splits):
-                reads, expected = walk(n, qlen, t0, 32, split, splits, int4, lead)
+                reads, expected = walk(n, qlen, t0, 32, split, splits, kernel["int4"], lead, kernel.get("wide", False))
                 assert reads == expected, (n, qlen, splits, t0, split)
 
 
-@pytest.mark.parametrize("int4", [True, False], ids=["int4", "int8"])
-def test_a_bound_one_tile_shorter_reads_past_the_row(int4):
+@pytest.mark.parametrize("kernel", KERNELS, ids=IDS)
+def test_a_bound_one_tile_shorter_reads_past_the_row(kernel):
     """The walk catches the mistake it guards against: steady iterations up to the split's last tile read the entry
     after a last tile of 1..16 keys."""
-    bad = out_of_row(steady_lead() - 1, int4)
+    bad = out_of_row(steady_lead() - 1, **kernel)
     assert bad, "the shorter bound should read past the row"
     assert all((n % 32) in range(1, 17) for n, *_ in bad)

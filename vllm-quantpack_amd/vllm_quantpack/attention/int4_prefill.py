@@ -57,8 +57,9 @@ def prefill_attention(q, k_cache, v_cache, k_scale_cache, v_scale_cache, out, *,
     When the chunk alone cannot fill the GPU, the keys are split over workgroups
     (num_splits, 0 = automatic) and merged; the fp32 partials go to a workspace from torch's caching allocator.
     max_seqlen_k bounds the automatic split count; without it the block table's capacity stands in (no host sync).
-    Head 512, or more than 12 query heads per KV head, runs the split-KV decode kernel over causal query slices of
-    the chunk and merges (the library picks the path)."""
+    More than 12 query heads per KV head run the library's wide kernel (rows as (token, head) pairs on 32x32x16
+    MFMAs); head 512 runs the split-KV decode kernel over causal query slices of the chunk and merges (the library
+    picks the path)."""
     hs = q.shape[2]
     cache = _hip.paged_cache(k_cache, v_cache, k_scale_cache, v_scale_cache, hs)
     if max_seqlen_k is None:

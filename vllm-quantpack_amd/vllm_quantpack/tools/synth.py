@@ -10,6 +10,8 @@ Workloads (24 query / 4 KV heads, head 256, block 16 unless stated):
   prefill-k8v4-128k-c1024  the prefill chunk workload over a k8v4 cache (int8 keys stored by the store as well)
   prefill-int4-h512-128k-c1024  the prefill chunk workload at head 512 with 16 query / 2 KV heads (the shape of a
                            Gemma-style global attention layer)
+  prefill-int4-g16-32k-c1024  a 1024-token chunk over 32768 cached tokens with 32 query / 2 KV heads (16 query heads
+                           per KV head), head 256
 
 int4 cells: nibbles uniform 0..15; per (token, KV head) fp32 scale ~ lognormal(-3, 0.5) with its low 4 mantissa bits
 replaced by the zero point round(U(6, 9)). k8v4 keys: int8 uniform -127..127, fp32 scale ~ lognormal(-4, 0.5).
@@ -24,7 +26,8 @@ import numpy as np
 NQ, NKV, HS, BS = 24, 4, 256, 16
 
 WORKLOADS = ("decode-int4-4k-t1", "decode-int4-128k-t2", "decode-int4-256k-t4", "prefill-int4-128k-c1024",
-             "decode-k8v4-ragged-b32", "prefill-k8v4-128k-c1024", "prefill-int4-h512-128k-c1024")
+             "decode-k8v4-ragged-b32", "prefill-k8v4-128k-c1024", "prefill-int4-h512-128k-c1024",
+             "prefill-int4-g16-32k-c1024")
 
 
 @dataclass
@@ -123,10 +126,11 @@ def make(name: str, *, small: bool = False) -> Workload:
         return _single(name, rng, 131072 // div, 2)
     if name == "decode-int4-256k-t4":
         return _single(name, rng, 262144 // div, 4)
-    if name in ("prefill-int4-128k-c1024", "prefill-k8v4-128k-c1024", "prefill-int4-h512-128k-c1024"):
+    if name in ("prefill-int4-128k-c1024", "prefill-k8v4-128k-c1024", "prefill-int4-h512-128k-c1024",
+                "prefill-int4-g16-32k-c1024"):
         k8v4 = name.startswith("prefill-k8v4")
-        nq, nkv, hs = (16, 2, 512) if "-h512-" in name else (NQ, NKV, HS)
-        cached, chunk = 131072 // div, 1024 // (4 if small else 1)
+        nq, nkv, hs = (16, 2, 512) if "-h512-" in name else (32, 2, HS) if "-g16-" in name else (NQ, NKV, HS)
+        cached, chunk = (32768 if "-32k-" in name else 131072) // div, 1024 // (4 if small else 1)
         n = cached + chunk
         nb = -(-n // BS)
         kv = fill_k8v4_cache(rng, nb, nkv, BS, hs) if k8v4 else fill_int4_cache(rng, nb, nkv, BS, hs)
