@@ -134,8 +134,10 @@ int qp_merge_segments(const qp_merge_args *args, qp_stream_t stream);
  * When the query blocks alone cannot fill the device, the keys of each block are split over workgroups
  * (num_splits, 0 = chosen for the device) whose fp32 partials go to the caller's workspace and are merged as in
  * qp_merge_segments; without enough workspace an automatic choice falls back to one split.
- * Head 512, or more than 12 query heads per KV head, runs the split-KV decode kernel over causal query slices of at
- * most 4 tokens and merges; that path needs the workspace (qp_prefill_workspace_size bytes, 256-byte aligned).
+ * More than 12 query heads per KV head run a wide variant whose 32-row MFMA tiles hold (token, head) pairs. Head 512
+ * with int4 keys runs that variant too, always with at least 2 splits; with int8 keys it runs the split-KV decode
+ * kernel over causal query slices of at most 4 tokens and merges. Both head-512 paths need the workspace
+ * (qp_prefill_workspace_size bytes, 256-byte aligned).
  * With rht_signs the result is rotated back, out = (o H D) * rht_out_scale, as qp_merge_segments does.
  * Replaces prefill_sequence (int4_prefill.py:203-232: unpack to bf16 segments + FlashAttention + LSE merge, with the
  * inverse single_rht of int4_kv.py:329) and the 2D path of the generated Triton kernel (int4_kv.py:113-118).

@@ -257,7 +257,7 @@ def test_inline_mfma_sources_are_scanned():
     assert build.has_inline_mfma('asm volatile("s_nop 1\\n\\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(x));')
     assert not build.has_inline_mfma('asm volatile("s_mov_b32 m0, %1\\n\\ts_nop 0" ::"s"(x));\n// v_mfma in a comment')
     csrc = os.path.join(os.path.dirname(build.__file__), "csrc")
-    for name in ("qp_decode.hip", "qp_prefill.hip"):
+    for name in ("qp_decode.hip", "qp_prefill.hip", "qp_prefill_wide.hip"):
         assert build.has_inline_mfma(open(os.path.join(csrc, name)).read()), name
 
 
@@ -281,32 +281,82 @@ def test_inline_mfma_wait_scan():
     assert len(scan(vdst)) == 1
 
 
-def test_spill_scan_flags_scratch_in_mfma_blocks():
-    """The build fails when spill code shares a basic block with MFMAs (the steady-state loop); spills stored before
-    the loop and reloaded on other blocks pass."""
-    scan = _build_module().spills_in_mfma_blocks
+def test_valu_write_before_inline_mfma_scan():
+    """The build's scan flags an inline-assembly MFMA that reads (as A, B or C) a register a VALU instruction wrote
+    fewer than 2 wait states before: the hardware then reads the register's previous contents. Two wait states (an
+    s_nop 1, or two other instructions) in between, a load's result, or the compiler's own MFMAs pass."""
+    build = _build_module()
+    scan = build.valu_writes_before_mfma
+    mfma = "v_mfma_f32_32x32x16_bf16 v[0:15], v[148:151], v[140:143], v[0:15]"
+    fresh = f"\tv_bitop3_b32 v150, v2, s53, v232 bitop3:0xea\n;;#ASMSTART\n\t{mfma}\n;;#ASMEND\n"
+    assert scan(fresh) == [(2, mfma, "v_bitop3_b32 v150, v2, s53, v232 bitop3:0xea")]
+    one = f"\tv_cvt_pk_bf16_f32 v143, v1, v2\n\ts_mov_b32 s0, 1\n;;#ASMSTART\n\t{mfma}\n;;#ASMEND\n"
+    assert len(scan(one)) == 1
+    acc = f"\tv_mov_b32 v3, 0\n;;#ASMSTART\n\t{mfma}\n;;#ASMEND\n"
+    assert len(scan(acc)) == 1  # the C operand counts too
+    waited = f"\tv_bitop3_b32 v150, v2, s53, v232 bitop3:0xea\n;;#ASMSTART\n\ts_nop 1\n\t{mfma}\n;;#ASMEND\n"
+    assert scan(waited) == []
+    apart = (f"\tv_bitop3_b32 v150, v2, s53, v232 bitop3:0xea\n\tv_add_u32 v200, v8, v7\n\ts_mov_b32 s0, 1\n"
+             f";;#ASMSTART\n\t{mfma}\n;;#ASMEND\n")
+    assert scan(apart) == []
+    other = f"\tv_bitop3_b32 v152, v2, s53, v232 bitop3:0xea\n;;#ASMSTART\n\t{mfma}\n;;#ASMEND\n"
+    assert scan(other) == []
+    load = f"\tds_read_b128 v[148:151], v1\n\ts_waitcnt lgkmcnt(0)\n;;#ASMSTART\n\t{mfma}\n;;#ASMEND\n"
+    assert scan(load) == []
+    assert scan(f"\tv_bitop3_b32 v150, v2, s53, v232 bitop3:0xea\n\t{mfma}\n") == []
+
+
+def test_spill_scan_flags_scratch_in_mfma_loops():
+    """The build fails when spill code runs in a loop that issues MFMAs with no MFMA loop inside it (the tile loop);
+    spills stored before it and reloaded after, in an outer loop around it (a pass restarted) or in an epilogue that
+    issues MFMAs pass. The listings follow the compiler's loop annotations."""
+    build = _build_module()
+    scan = build.spills_in_mfma_loops
     mfma = "\tv_mfma_f32_16x16x32_bf16 v[0:3], v[4:7], v[8:11], 0\n"
-    hot = f"kern:\n.LBB0_1:                                ; in Loop\n{mfma}\tscratch_load_dword v5, off, off ; Reload\n"
-    assert scan(hot) == [("kern", ".LBB0_1", "scratch_load_dword v5, off, off")]
-    cold = (f"kern:\n\tscratch_store_dword off, v5, off\n.LBB0_1:\n{mfma}\ts_cbranch_scc1 .LBB0_1\n"
-            ".LBB0_2:\n\tscratch_load_dword v5, off, off\n")
+    spill = "\tscratch_load_dword v5, off, off ; Reload\n"
+    hot = (f"kern:\n.LBB0_1:                                ; =>This Inner Loop Header: Depth=1\n{mfma}"
+           f"\ts_cbranch_scc1 .LBB0_2\n; %bb.2:                                ; in Loop: Header=BB0_1 Depth=1\n{spill}"
+           "\ts_branch .LBB0_1\n")
+    assert scan(hot) == [("kern", "%bb.2", "scratch_load_dword v5, off, off")]
+    cold = (f"kern:\n\tscratch_store_dword off, v5, off\n.LBB0_1:                                ; =>This Inner Loop "
+            f"Header: Depth=1\n{mfma}\ts_cbranch_scc1 .LBB0_1\n.LBB0_2:\n{mfma}{spill}")
     assert scan(cold) == []
-    # a new function resets the block state; comment lines are not labels
-    two = f"k1:\n{mfma}; %bb.3:\nk2:\n\tscratch_load_dword v5, off, off\n"
+    # a pass loop (depth 1) around the tile loop (depth 2): its own MFMAs and spills are once per pass
+    nested = (f"kern:\n.LBB0_1:                                ; =>This Loop Header: Depth=1\n{mfma}{spill}"
+              f".LBB0_2:                                ;   Parent Loop BB0_1 Depth=1\n"
+              f"                                        ; =>  This Inner Loop Header: Depth=2\n{mfma}"
+              "\ts_cbranch_scc1 .LBB0_2\n; %bb.3:                                ; in Loop: Header=BB0_1 Depth=1\n"
+              f"{spill}\ts_branch .LBB0_1\n")
+    assert scan(nested) == []
+    assert build.mfma_loops(nested) == {"kern": {"BB0_2"}}
+    # a tile loop holding a small loop without MFMAs (a gather) is still the MFMA loop
+    gather = (f"kern:\n.LBB0_1:                                ; =>This Loop Header: Depth=1\n{mfma}{spill}"
+              ".LBB0_2:                                ;   Parent Loop BB0_1 Depth=1\n"
+              "                                        ; =>  This Inner Loop Header: Depth=2\n"
+              "\ts_cbranch_scc1 .LBB0_2\n")
+    assert scan(gather) == [("kern", ".LBB0_1", "scratch_load_dword v5, off, off")]
+    # a new function resets the block state
+    two = f"k1:\n.LBB0_1:                                ; =>This Inner Loop Header: Depth=1\n{mfma}k2:\n{spill}"
     assert scan(two) == []
 
 
-def test_built_kernels_keep_spills_off_the_mfma_blocks():
-    """Every kernel source with MFMAs, compiled as the build does, has no spill code in an MFMA block."""
+def test_built_kernels_keep_spills_off_the_mfma_loops():
+    """Every kernel source with MFMAs, compiled as the build does, has an MFMA loop in each of its MFMA kernels, no
+    spill code in one, and the wait states its inline MFMAs need."""
     import shutil
-    import subprocess
     build = _build_module()
     if shutil.which(build.hipcc()) is None and not os.path.exists(build.hipcc()):
         pytest.skip("no hipcc")
-    asm = os.path.join(build.OBJ, "qp_prefill.gfx.s")
+    asm = os.path.join(build.OBJ, "qp_prefill_wide.gfx.s")
     if not os.path.exists(asm):
         pytest.skip("not built")
-    for name in ("qp_decode", "qp_prefill"):
+    for name in ("qp_decode", "qp_prefill", "qp_prefill_wide"):
         text = open(os.path.join(build.OBJ, f"{name}.gfx.s")).read()
         assert "v_mfma" in text
-        assert build.spills_in_mfma_blocks(text) == [], name
+        assert build.spills_in_mfma_loops(text) == [], name
+        assert build.mfma_hazards(text) == [], name
+        assert build.valu_writes_before_mfma(text) == [], name
+        loops = build.mfma_loops(text)
+        kernels = [fn for fn in loops if "decode_" in fn or "prefill_" in fn]
+        assert kernels, name
+        assert all(loops[fn] for fn in kernels), [fn for fn in kernels if not loops[fn]]

@@ -742,9 +742,10 @@ def test_prefill_block_sizes_and_gqa(device, bs):
 
 
 @pytest.mark.parametrize("fmt", ["int4", "int8"])
-def test_prefill_head_512_query_slices(device, fmt):
-    """Head 512 prefills through the split-KV kernel over causal query slices, then the merge (the reference keeps
-    these on its Triton kernel: tests/test_int4_kv.py:194-210, tests/test_k8v4_kv.py:208-225). Ragged batch."""
+def test_prefill_head_512(device, fmt):
+    """Head 512: int4 keys take the wide kernel (K operands from the packed codes, always key-split), int8 keys the
+    split-KV kernel over causal query slices, then the merge (the reference keeps these on its Triton kernel:
+    tests/test_int4_kv.py:194-210, tests/test_k8v4_kv.py:208-225). Ragged batch."""
     rng = np.random.default_rng(401 + (1 if fmt == "int8" else 0))
     out, emu, ref = _prefill_case(device, rng, fmt, [(37, 2100), (5, 600), (1, 64)], nq=16, nkv=2, hs=512)
     assert_emulation(out, emu)
@@ -761,11 +762,12 @@ def test_prefill_wide_gqa(device):
 
 
 @pytest.mark.parametrize("fmt", ["int4", "int8"])
-@pytest.mark.parametrize("hs,splits", [(256, 1), (256, 3), (128, 1), (128, 2)])
+@pytest.mark.parametrize("hs,splits", [(256, 1), (256, 3), (128, 1), (128, 2), (512, 1), (512, 3)])
 def test_prefill_wide_kernel_batches(device, fmt, hs, splits):
-    """The wide kernel on a batch whose row blocks (128 rows at head 256, 256 at head 128) straddle tokens and end
-    mid-block: a long chunk, a first chunk (context == chunk), a single token, a 130-token chunk; 32 query heads on 2
-    KV heads; with key splits, some of them empty."""
+    """The wide kernel on a batch whose row blocks (128 rows at heads 256 and 512, 256 at head 128) straddle tokens
+    and end mid-block: a long chunk, a first chunk (context == chunk), a single token, a 130-token chunk; 32 query heads
+    on 2 KV heads; with key splits, some of them empty (head 512 runs at least 2; with int8 keys it takes the query
+    slices)."""
     rng = np.random.default_rng(260 + hs + splits + (1 if fmt == "int8" else 0))
     lens = [(40, 3000), (7, 7), (1, 500), (130, 900)]
     out, emu, ref = _prefill_case(device, rng, fmt, lens, nq=32, nkv=2, hs=hs, splits=splits)
@@ -774,36 +776,40 @@ def test_prefill_wide_kernel_batches(device, fmt, hs, splits):
     assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
 
 
-@pytest.mark.parametrize("fmt,n", [("int4", 330), ("int8", 1000)])
-def test_prefill_wide_table_row_exactly_as_long_as_the_context(device, fmt, n):
+@pytest.mark.parametrize("fmt,n,hs", [("int4", 330, 256), ("int8", 1000, 256), ("int4", 1009, 512), ("int4", 353, 512)])
+def test_prefill_wide_table_row_exactly_as_long_as_the_context(device, fmt, n, hs):
     """One sequence whose block table holds exactly ceil(n / 16) entries and whose last tile has 1..16 keys, on the
     wide kernel (the CPU walk in test_prefill_table_walk checks its table reads)."""
     rng = np.random.default_rng(270 + n)
-    out, emu, ref = _prefill_case(device, rng, fmt, [(20, n)], nq=16, nkv=1)
+    out, emu, ref = _prefill_case(device, rng, fmt, [(20, n)], nq=16, nkv=1, hs=hs)
     assert_emulation(out, emu)
     assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
 
 
-@pytest.mark.parametrize("fmt", ["int4", "int8"])
-def test_prefill_wide_scores_far_above_the_first_tile(device, fmt):
+@pytest.mark.parametrize("fmt,hs", [("int4", 256), ("int8", 256), ("int4", 512)])
+def test_prefill_wide_scores_far_above_the_first_tile(device, fmt, hs):
     """Key scales of 2^7 .. 2^12 late in the context put scores thousands of log2 units above the first tile's
     maximum, past the wide kernel's headroom: the workgroup runs its split again with the raised maxima (once per
     jump), and the result still matches."""
-    rng = np.random.default_rng(280 + (1 if fmt == "int8" else 0))
+    rng = np.random.default_rng(280 + (1 if fmt == "int8" else 0) + hs)
     big = [(700, 2.0 ** 7), (1300, 2.0 ** 9), (1901, 2.0 ** 12)]
-    out, emu, ref = _prefill_case(device, rng, fmt, [(40, 2000), (9, 1400)], nq=16, nkv=1, splits=1, big_keys=big)
+    out, emu, ref = _prefill_case(device, rng, fmt, [(40, 2000), (9, 1400)], nq=16, nkv=1, hs=hs, splits=1,
+                                  big_keys=big)
     assert np.isfinite(out).all()
     assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
 
 
-def test_prefill_wide_fused_rotations(device):
+@pytest.mark.parametrize("hs", [256, 512])
+def test_prefill_wide_fused_rotations(device, hs):
     """On the wide kernel: the query rotated on load gives the bits of rotating it first, and the output rotated back
-    in the epilogue (one split) or by the merge (three) matches a separate inverse rotation."""
+    in the epilogue (one split) or by the merge (three; at head 512 the kernel always splits) matches a separate
+    inverse rotation."""
     import torch
 
     from vllm_quantpack.attention import int4_prefill, rht
-    rng = np.random.default_rng(290)
+    rng = np.random.default_rng(290 + hs)
     n, qlen, bs, nq, nkv = 2500, 50, 16, 32, 2
+    HS = hs
     nb = -(-n // bs)
     kv, _ = random_cache(rng, nb, nkv, bs, HS)
     _, (kc, vc, ks, vs) = torch_cache(kv, HS, "int4", device)
@@ -826,10 +832,13 @@ def test_prefill_wide_fused_rotations(device):
         assert O.relerr(to_f32(got), want) < 1e-2, splits
 
 
-def test_prefill_span_and_row_loaders_agree(device):
-    """The page-run copies (HND) and the strided gather (NHD) of the prefill kernel on the same cache contents."""
-    a, emu, ref = _prefill_case(device, np.random.default_rng(204), "int8", [(64, 1500), (3, 700)])
-    b, _, _ = _prefill_case(device, np.random.default_rng(204), "int8", [(64, 1500), (3, 700)], layout="nhd")
+@pytest.mark.parametrize("fmt,hs,nq", [("int8", 256, NQ), ("int4", 512, 16)])
+def test_prefill_span_and_row_loaders_agree(device, fmt, hs, nq):
+    """The page-run copies (HND) and the strided gather (NHD) of the prefill kernel (and at head 512 the wide one) on
+    the same cache contents."""
+    case = dict(hs=hs, nq=nq, nkv=2 if hs == 512 else NKV)
+    a, emu, ref = _prefill_case(device, np.random.default_rng(204), fmt, [(64, 1500), (3, 700)], **case)
+    b, _, _ = _prefill_case(device, np.random.default_rng(204), fmt, [(64, 1500), (3, 700)], layout="nhd", **case)
     assert_emulation(a, emu)
     assert_emulation(b, emu)
     assert O.relerr(a, b) < 5e-3

@@ -111,36 +111,118 @@ def mfma_hazards(asm):
     return found
 
 
+VALU_WAIT = 2  # wait states between a VALU write of a VGPR and an MFMA reading it as a source
+
+
+def valu_writes_before_mfma(asm):
+    """[(line, mfma, writer)] of inline-assembly MFMAs that read a register (A, B or C) that a VALU instruction wrote
+    fewer than VALU_WAIT wait states before. The compiler inserts these waits for its own MFMAs only; without them
+    the MFMA reads the register's previous contents."""
+    ins = []
+    inline = False
+    for i, raw in enumerate(asm.splitlines()):
+        l = raw.strip()
+        if l.startswith(";;#ASMSTART"):
+            inline = True
+        elif l.startswith(";;#ASMEND"):
+            inline = False
+        elif l and not l.startswith((";", ".")) and not raw.startswith((".", "_")):
+            ins.append((i, l.split(";")[0].strip(), inline))
+    found = []
+    for k, (i, line, inl) in enumerate(ins):
+        if not (inl and line.startswith("v_mfma")):
+            continue
+        srcs = _vregs(",".join(a.strip() for a in line.split(None, 1)[1].split(",")[1:4]))
+        waits = 0
+        for _, prev, _ in reversed(ins[max(0, k - VALU_WAIT):k]):
+            op = prev.split()[0]
+            if op == "s_nop":
+                waits += int(prev.split()[1]) + 1
+            else:
+                if op.startswith("v_") and not op.startswith("v_mfma") and " " in prev:
+                    if _vregs(prev.split(None, 1)[1].split(",")[0]) & srcs:
+                        found.append((i, line, prev))
+                        break
+                waits += 1
+            if waits >= VALU_WAIT:
+                break
+    return found
+
+
 _FUNC = re.compile(r"^[A-Za-z_][\w.$]*:")
 _BLOCK = re.compile(r"^\.LBB\d+_\d+:")
 
 
-def spills_in_mfma_blocks(asm):
-    """[(function, block, instruction)] of scratch accesses in basic blocks that also issue MFMAs. Kernels whose
-    register state spills at all must keep the spill code off the MFMA loop (where it is stored once and reloaded on
-    rare paths), and this check holds them to it."""
-    found = []
-    fn = block = None
-    has_mfma, scratch = False, []
+_LOOP_HEADER = re.compile(r"=>\s*This (?:Inner )?Loop Header: Depth=\d+")
+_IN_LOOP = re.compile(r"in Loop: Header=(BB\d+_\d+) Depth=\d+")
+_PARENT_LOOP = re.compile(r"Parent Loop (BB\d+_\d+) Depth=\d+")
 
-    def close():
-        if has_mfma:
-            found.extend((fn, block, s) for s in scratch)
 
+def _loop_blocks(asm):
+    """[(function, blocks, MFMA loops)] of an assembly listing: each block as a dict (name, innermost loop, scratch
+    accesses), and the loops that issue MFMAs in their own blocks with no loop inside them that does (a tile loop,
+    whatever small loops it holds). From the compiler's loop annotations: a block heading a loop is marked `=> This
+    [Inner] Loop Header`, a nested one after `Parent Loop BBf_n` lines from the outermost loop in, and the other blocks
+    of a loop `in Loop: Header=BBf_n` after the innermost loop holding them."""
+    out = []
+
+    def close(fn, blocks):
+        parent = {b["name"][2:]: b["parent"] for b in blocks if b["head"]}
+        mfma = {b["loop"] for b in blocks if b["mfma"] and b["loop"]}
+        nested = set()
+        for loop in mfma:  # a loop holding an MFMA loop is not one itself
+            up = parent.get(loop)
+            while up:
+                nested.add(up)
+                up = parent.get(up)
+        out.append((fn, blocks, mfma - nested))
+
+    def block(name):
+        return {"name": name, "loop": None, "head": False, "parent": None, "mfma": False, "scratch": []}
+
+    fn, blocks, cur = None, [], None
     for raw in asm.splitlines():
         l = raw.strip()
         if _FUNC.match(raw):
-            close()
-            fn, block, has_mfma, scratch = raw.split(":")[0], "entry", False, []
-        elif _BLOCK.match(l):
-            close()
-            block, has_mfma, scratch = l.split(":")[0], False, []
-        elif l.startswith("v_mfma"):
-            has_mfma = True
+            if fn is not None:
+                close(fn, blocks)
+            fn = raw.split(":")[0]
+            cur = block("entry")
+            blocks = [cur]
+            continue
+        if cur is None:
+            continue
+        if _BLOCK.match(l) or l.startswith("; %bb."):
+            cur = block(l.split(":")[0].lstrip("; "))
+            blocks.append(cur)
+        if _LOOP_HEADER.search(raw):  # heads a loop: its own, inside the last parent marked before (if any)
+            cur["parent"], cur["loop"], cur["head"] = cur["parent"] or cur["loop"], cur["name"][2:], True
+        elif _PARENT_LOOP.search(raw):
+            cur["parent"] = _PARENT_LOOP.search(raw).group(1)
+        else:
+            m = _IN_LOOP.search(raw)
+            if m and cur["loop"] is None:
+                cur["loop"] = m.group(1)
+        if l.startswith("v_mfma"):
+            cur["mfma"] = True
         elif l.startswith("scratch_"):
-            scratch.append(l.split(";")[0].strip())
-    close()
-    return found
+            cur["scratch"].append(l.split(";")[0].strip())
+    if fn is not None:
+        close(fn, blocks)
+    return out
+
+
+def mfma_loops(asm):
+    """{function: its MFMA loops (header block names)}."""
+    return {fn: hot for fn, _, hot in _loop_blocks(asm)}
+
+
+def spills_in_mfma_loops(asm):
+    """[(function, block, instruction)] of scratch accesses in the MFMA loops. Kernels whose register state spills at
+    all must keep the spill code off those loops: stored before them and reloaded after, or on an outer loop's path
+    (a pass restarted) or in an epilogue, which run once per loop rather than per tile; this check holds them to it."""
+    return [(fn, b["name"], x) for fn, blocks, hot in _loop_blocks(asm) for b in blocks if b["loop"] in hot
+            for x in b["scratch"]]
 
 
 def has_inline_mfma(text):
@@ -164,10 +246,14 @@ def _check_inline_mfma(src, verbose):
     if bad:
         lines = "\n".join(f"  {a}: {b}  ->  {c}" for a, b, c in bad[:10])
         raise RuntimeError(f"{src}: MFMA results read within {MFMA_WAIT} wait states:\n{lines}")
-    spills = spills_in_mfma_blocks(asm)
+    bad = valu_writes_before_mfma(asm)
+    if bad:
+        lines = "\n".join(f"  {a}: {c}  ->  {b}" for a, b, c in bad[:10])
+        raise RuntimeError(f"{src}: MFMA sources written by the VALU within {VALU_WAIT} wait states:\n{lines}")
+    spills = spills_in_mfma_loops(asm)
     if spills:
         lines = "\n".join(f"  {f} {b}: {i}" for f, b, i in spills[:10])
-        raise RuntimeError(f"{src}: spill code in MFMA blocks:\n{lines}")
+        raise RuntimeError(f"{src}: spill code in an MFMA loop:\n{lines}")
 
 
 def build(jobs=None, verbose=False, only=None):

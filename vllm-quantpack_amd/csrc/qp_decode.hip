@@ -798,9 +798,11 @@ __device__ __forceinline__ void load_rows(ChunkRegs<Sh> &r, const DecodeParams &
   if (lane_valid) {
     const int b = hc ? bid[1] : bid[0];
     const int slot = (hc ? slot0[1] : slot0[0]) + (kk & 15);
-    const uint32_t *base = is_v ? p.vwords : p.kwords;
-    const int64_t s0 = is_v ? p.vws0 : p.kws0, s1 = is_v ? p.vws1 : p.kws1, s2 = is_v ? p.vws2 : p.kws2;
-    r.w = base[(int64_t)b * s0 + (int64_t)slot * s1 + (int64_t)h * s2];
+    // Both offsets from the wave-uniform strides, one pointer chosen per lane: selecting the strides per lane instead
+    // keeps six 64-bit lane values live across the loop, which spill at head 512.
+    const uint32_t *kw = p.kwords + ((int64_t)b * p.kws0 + (int64_t)slot * p.kws1 + (int64_t)h * p.kws2);
+    const uint32_t *vw = p.vwords + ((int64_t)b * p.vws0 + (int64_t)slot * p.vws1 + (int64_t)h * p.vws2);
+    r.w = *(is_v ? vw : kw);
   }
 }
 

@@ -69,7 +69,9 @@ struct PfShape {
   static constexpr int kOffV = kOffK + 2 * kKd;
   static constexpr int kLds = kOffV + 3 * kVb;
   static_assert(kKd % 16 == 0 && kVt % 16 == 0 && kVb % 16 == 0, "alignment");
-  static_assert(kLds <= 160 * 1024, "LDS");
+  // the tile kernel's buffers fit up to head 256; at head 512 only the cell and copy geometry is used (the wide
+  // kernel, with its own LDS plan)
+  static_assert(HS > 256 || kLds <= 160 * 1024, "LDS");
 };
 
 // Block-table indices of the two page runs of the tile at key k0 (a run at or past kend repeats run 0, so only valid
@@ -208,8 +210,8 @@ __device__ __forceinline__ u32x2_t i8_quad_bf16(uint32_t x) {
                  pack_bf16x2((float)((u >> 16) & 0xFFu), (float)(u >> 24))};
 }
 
-// The prefill on 32x32x16 MFMAs (qp_prefill_wide.hip), head 128 or 256: grid (row blocks of prefill_wide_rows(head
-// size) (token, query head) pairs, KV heads, key splits).
+// The prefill on 32x32x16 MFMAs (qp_prefill_wide.hip), head 128 or 256, or 512 with int4 keys (at least 2 key
+// splits): grid (row blocks of prefill_wide_rows(head size) (token, query head) pairs, KV heads, key splits).
 int prefill_wide_rows(int head_size);
 void prefill_wide(const PrefillParams &p, int head_size, int key_format, dim3 grid, bool span, hipStream_t s);
 

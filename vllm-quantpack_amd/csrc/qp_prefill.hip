@@ -244,6 +244,16 @@ __device__ __forceinline__ void pv_step(f32x4_t (&acc)[NT][17], int b, bf16x8_t 
   }
 }
 
+// Two wait states between the VALU instructions that packed the P operands and the first PV MFMA reading them (the
+// compiler inserts these for its own MFMAs only). The operands pass through this statement, so every write of them
+// comes before it.
+template <int NT>
+__device__ __forceinline__ void p_ready(u32x4_t (&pop)[NT]) {
+  if constexpr (NT == 1) asm volatile("s_nop 1" : "+v"(pop[0]));
+  else if constexpr (NT == 2) asm volatile("s_nop 1" : "+v"(pop[0]), "+v"(pop[1]));
+  else asm volatile("s_nop 1" : "+v"(pop[0]), "+v"(pop[1]), "+v"(pop[2]));
+}
+
 // one QK step (32 channels of one 16-key sub-tile) for every row tile of the wave
 template <int HS, int NT>
 __device__ __forceinline__ void qk_step(f32x4_t (&d)[NT][2], int sub, int mi, bf16x8_t kop,
@@ -405,6 +415,7 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
   // ---- phase B
 #pragma unroll
   for (int b = 0; b < kPreV; ++b) vbuf[b] = *reinterpret_cast<const bf16x8_t *>(vaddr(b));
+  p_ready<NT>(pop);
   auto at = [&](int b, int x) { return b == (x < kP - 1 ? x : kP - 1); };
 #pragma unroll
   for (int b = 0; b < kP; ++b) {
@@ -810,23 +821,26 @@ void dispatch_nt(const PrefillParams &p, int nt, dim3 grid, bool span, hipStream
 }
 
 // Which kernel serves a prefill: the 16-row-tile kernel above up to 12 query heads per KV head; the wide kernel
-// (qp_prefill_wide.hip: 128 or 256 (token, head) rows per workgroup on 32x32x16 MFMAs, any GQA width) above that; the
-// query-slice path for head 512. (At head 256 the wide kernel holds one 32-row tile per wave, so each K / V operand it
-// reads from LDS serves 32 rows against the tile kernel's 48: 6.3 against 3.3 ms on the 1024-token chunk over 131072
-// keys with 6 query heads per KV head.)
+// (qp_prefill_wide.hip: 128 or 256 (token, head) rows per workgroup on 32x32x16 MFMAs, any GQA width) above that and
+// for head 512 with int4 keys; the query-slice path for head 512 with int8 keys, whose 776-byte cells do not fit the
+// wide kernel's LDS plan. (At head 256 the wide kernel holds one 32-row tile per wave, so each K / V operand it reads
+// from LDS serves 32 rows against the tile kernel's 48: 6.3 against 3.3 ms on the 1024-token chunk over 131072 keys
+// with 6 query heads per KV head.)
 enum class PrefillPath { kSlices, kTiles, kWide };
 
 PrefillPath prefill_path(const qp_paged_cache *cache, const qp_prefill_args *a) {
   const int hs = cache->head_size;
+  if (hs == 512) return cache->key.format == QP_CODES_INT4 ? PrefillPath::kWide : PrefillPath::kSlices;
   if (hs != 128 && hs != 256) return PrefillPath::kSlices;
   return a->num_q_heads / cache->num_kv_heads > 12 ? PrefillPath::kWide : PrefillPath::kTiles;
 }
 
 // Key splits of the wide kernel: the count whose workgroups (row blocks x KV heads x splits) fill the CUs in the
 // fewest rounds per unit of work, each split keeping >= 1024 keys (192 workgroups on 256 CUs: 4 splits, 3 full
-// rounds).
+// rounds). At head 512 at least 2: that kernel writes split partials only, and the merge rotates and normalises.
 int wide_splits(const qp_paged_cache *cache, const qp_prefill_args *a) {
-  if (a->num_splits > 0) return a->num_splits;
+  const int min_s = cache->head_size == 512 ? 2 : 1;
+  if (a->num_splits > 0) return a->num_splits > min_s ? a->num_splits : min_s;
   const int G = a->num_q_heads / cache->num_kv_heads;
   const int rows = prefill_wide_rows(cache->head_size);
   const int64_t blocks = ((int64_t)a->num_tokens * G + rows - 1) / rows;
@@ -834,10 +848,10 @@ int wide_splits(const qp_paged_cache *cache, const qp_prefill_args *a) {
   const int64_t cus = device_cus();
   int max_s = a->max_seqlen_k / 1024;
   if (max_s > 64) max_s = 64;
-  if (max_s < 1) max_s = 1;
-  int best = 1;
-  double best_cost = (double)((wgs + cus - 1) / cus);
-  for (int S = 2; S <= max_s; ++S) {
+  if (max_s < min_s) max_s = min_s;
+  int best = min_s;
+  double best_cost = (double)((wgs * min_s + cus - 1) / cus) / min_s;
+  for (int S = min_s + 1; S <= max_s; ++S) {
     const double cost = (double)((wgs * S + cus - 1) / cus) / S;
     if (cost < best_cost - 1e-9) {
       best = S;
@@ -900,6 +914,8 @@ int prefill_run(const qp_paged_cache *cache, const qp_prefill_args *a, const int
     QP_REQUIRE(a->num_splits == 0, "qp_prefill: workspace too small for the requested splits");
     splits = 1;  // automatic choice without (enough) workspace: one workgroup per query block and KV head
   }
+  QP_REQUIRE(!wide || hs != 512 || splits > 1,
+             "qp_prefill: head 512 needs a workspace of qp_prefill_workspace_size bytes (split partials)");
   QP_REQUIRE(splits == 1 || aligned(a->workspace, 16), "qp_prefill: workspace must be 16-byte aligned");
 
   PrefillParams p;

@@ -46,38 +46,52 @@ constexpr int kWidePasses = 8;         // passes over a split at most (each rais
 template <int HS, int KFMT>
 struct WShape {
   using Pf = PfShape<HS, KFMT>;
+  // Head 512 (int4 keys): bf16 K rows do not fit beside the V^T buffers, so each wave builds its QK operands from the
+  // packed codes (K direct), V is unpacked one tile ahead into two buffers and the per-key scalars two tiles ahead into
+  // a ring of two, and the packed slots (4) hold the tiles from the one being read to the one being copied.
+  static constexpr bool kDirect = HS == 512;
+  static_assert(!kDirect || KFMT == QP_CODES_INT4, "head 512 takes int4 keys");
   static constexpr int kKeyBytes = Pf::kKeyBytes;
   static constexpr int kCell = Pf::kCell;
+  static constexpr int kSlot = kDirect ? 32 * kCell : Pf::kPk;  // one packed slot (two 16-cell page runs)
+  static constexpr int kSlots = kDirect ? 4 : 3;
   static constexpr int kKdRow = HS * 2 + 16;       // bf16 K row + 16 bytes: 32 rows at one column hit 32 bank quads
   static constexpr int kKd = kPfKeys * kKdRow;
   static constexpr int kVtRow = kPfKeys * 2 + 16;  // 80 B: 32 rows x 16 B reads at one column are conflict-free
   static constexpr int kVt = HS * kVtRow;
-  // per-key scalars after the V^T rows: a_k, e_k, s_v (fp32 [32] each), then bf16 16 + zp_v in lane order [32], then
-  // a dummy slot for the threads that own no key
-  static constexpr int kOffA = kVt, kOffE = kVt + 128, kOffS = kVt + 256, kOffZ = kVt + 384, kOffDummy = kVt + 448;
-  static constexpr int kVb = (kOffDummy + 32 + 15) / 16 * 16;
-  static constexpr int kOffK = 3 * Pf::kPk;         // 3 packed slots, 2 K buffers, 3 V buffers
-  static constexpr int kOffV = kOffK + 2 * kKd;
-  static constexpr int kLds = kOffV + 3 * kVb;
-  static_assert(kKd % 16 == 0 && kVb % 16 == 0, "alignment");
+  // per-key scalars of a tile: a_k, e_k, s_v (fp32 [32] each), then bf16 16 + zp_v in lane order [32], then a dummy
+  // slot for the threads that own no key; after the V^T rows of the tile's V buffer, or in the ring (K direct)
+  static constexpr int kScA = 0, kScE = 128, kScS = 256, kScZ = 384, kScDummy = 448, kSc = 512;
+  static constexpr int kVb = kDirect ? kVt : kVt + kSc;
+  static constexpr int kVbufs = kDirect ? 2 : 3;
+  static constexpr int kOffK = kSlots * kSlot;      // packed slots, 2 K buffers (not K direct), V buffers, the ring
+  static constexpr int kOffV = kOffK + (kDirect ? 0 : 2 * kKd);
+  static constexpr int kOffR = kOffV + kVbufs * kVb;
+  static constexpr int kLds = kOffR + (kDirect ? 2 * kSc : 0);
+  static_assert(kSlot % 16 == 0 && kKd % 16 == 0 && kVb % 16 == 0, "alignment");
   static_assert(kLds <= 160 * 1024, "LDS");
   // key of PV slot s (0..15) of K step ks for lane half h: the S^T row order of the 32x32 accumulator
   static constexpr __host__ __device__ int slot_key(int ks, int h, int s) { return 16 * ks + (s < 4 ? 4 * h + s : 4 + 4 * h + s); }
+  // first channel (in K operand order) of QK step cs for lane half h: consecutive code dwords of a key go to the
+  // lane's consecutive steps when the operands come from the packed codes, so one 8-byte read serves two steps
+  static constexpr __host__ __device__ int step_chan(int cs, int h) { return kDirect ? 8 * (HS / 16 * h + cs) : 16 * cs + 8 * h; }
 };
 
 // Position of key kk's 16 + zp_v in the lane-ordered zero-point row: lane half h reads its 16 keys' values as i = 0..15
 // (key 8 (i / 4) + 4 h + i % 4) from 32 bytes at 32 h.
 __host__ __device__ constexpr int zp_pos(int kk) { return 16 * ((kk >> 2) & 1) + 4 * (kk >> 3) + (kk & 3); }
 
-// The unpack of one tile, cut into stages that the QK phase spreads over its MFMA steps.
+// The unpack of one tile, cut into stages that the QK phase spreads over its MFMA steps. The per-key scalars come from
+// slot pks into block sc (the same tile as the codes, or two tiles ahead of V with K direct).
 template <int HS, int KFMT>
 struct WStager {
   using Sh = WShape<HS, KFMT>;
   static constexpr int kKDw = KFMT == QP_CODES_INT4 ? HS / 8 : HS / 4;  // code dwords per key
   static constexpr int kNK = kPfKeys * kKDw / (kPfWaves * 64);           // K dwords per thread
-  const uint8_t *pk;
-  uint8_t *kd, *vt;
-  int k0, kend, tid;
+  static constexpr int kVUnits = HS > kPfWaves * 64 ? HS / (kPfWaves * 64) : 1;  // V units per thread
+  const uint8_t *pk, *pks;
+  uint8_t *kd, *vt, *sc;
+  int k0, kend, tid, vu;
   bool full;
   float scale_log2;
   uint32_t kx[kNK];
@@ -102,28 +116,28 @@ struct WStager {
     }
   }
   // V unit u = (channel quad q4, K step ks, lane half h) = (u >> 2, (u >> 1) & 1, u & 1): the four channel rows of q4
-  // at the 8 PV slots of (ks, h), i.e. keys slot_key(ks, h, 0..7)
-  __device__ __forceinline__ int vunit() const { return tid & (HS - 1); }
+  // at the 8 PV slots of (ks, h), i.e. keys slot_key(ks, h, 0..7). Unit j of the thread: tid + 256 j (mod HS).
+  __device__ __forceinline__ void v_unit(int j) { vu = (tid + kPfWaves * 64 * j) & (HS - 1); }
   __device__ __forceinline__ void v_load(int s) {
-    const int u = vunit(), q4 = u >> 2;
+    const int u = vu, q4 = u >> 2;
     const int ka = Sh::slot_key((u >> 1) & 1, u & 1, 2 * s);
     const uint8_t *src = pk + Sh::kKeyBytes + 4 + ka * Sh::kCell + 4 * (q4 >> 1);
     vx[2 * s] = *reinterpret_cast<const uint32_t *>(src);
     vx[2 * s + 1] = *reinterpret_cast<const uint32_t *>(src + Sh::kCell);
   }
   __device__ __forceinline__ void v_perm(int s) {
-    const int q4 = vunit() >> 2;
+    const int q4 = vu >> 2;
     pr[s] = __builtin_amdgcn_perm(vx[2 * s + 1], vx[2 * s], (q4 & 1) ? 0x07060302u : 0x05040100u);
   }
   __device__ __forceinline__ void v_store(int c) {
-    const int u = vunit(), q4 = u >> 2;
+    const int u = vu, q4 = u >> 2;
     *reinterpret_cast<u32x4_t *>(vt + (4 * q4 + c) * Sh::kVtRow + 16 * (u & 3)) =
         u32x4_t{nib_pair16(pr[0], c), nib_pair16(pr[1], c), nib_pair16(pr[2], c), nib_pair16(pr[3], c)};
   }
   __device__ __forceinline__ void s_load() {
     const int kk = tid & (kPfKeys - 1);
-    kw = *reinterpret_cast<const uint32_t *>(pk + kk * Sh::kCell + Sh::kKeyBytes);
-    vw = *reinterpret_cast<const uint32_t *>(pk + kk * Sh::kCell + Sh::kCell - 4);
+    kw = *reinterpret_cast<const uint32_t *>(pks + kk * Sh::kCell + Sh::kKeyBytes);
+    vw = *reinterpret_cast<const uint32_t *>(pks + kk * Sh::kCell + Sh::kCell - 4);
   }
   __device__ __forceinline__ void s_store() {
     const int kk = tid & (kPfKeys - 1);
@@ -137,33 +151,49 @@ struct WStager {
       e = a * 128.f;  // the operands are 128 + k
     }
     const bool own = tid < kPfKeys;
-    float *dummy = reinterpret_cast<float *>(vt + Sh::kOffDummy);
-    *(own ? reinterpret_cast<float *>(vt + Sh::kOffA) + kk : dummy) = ok ? a : 0.f;
-    *(own ? reinterpret_cast<float *>(vt + Sh::kOffE) + kk : dummy + 1) = ok ? e : 0.f;
-    *(own ? reinterpret_cast<float *>(vt + Sh::kOffS) + kk : dummy + 2) = ok ? __uint_as_float(vw & 0xFFFFFFF0u) : 0.f;
-    *(own ? reinterpret_cast<uint16_t *>(vt + Sh::kOffZ) + zp_pos(kk) : reinterpret_cast<uint16_t *>(dummy + 3)) =
+    float *dummy = reinterpret_cast<float *>(sc + Sh::kScDummy);
+    *(own ? reinterpret_cast<float *>(sc + Sh::kScA) + kk : dummy) = ok ? a : 0.f;
+    *(own ? reinterpret_cast<float *>(sc + Sh::kScE) + kk : dummy + 1) = ok ? e : 0.f;
+    *(own ? reinterpret_cast<float *>(sc + Sh::kScS) + kk : dummy + 2) = ok ? __uint_as_float(vw & 0xFFFFFFF0u) : 0.f;
+    *(own ? reinterpret_cast<uint16_t *>(sc + Sh::kScZ) + zp_pos(kk) : reinterpret_cast<uint16_t *>(dummy + 3)) =
         ok ? (uint16_t)(0x4180u | ((vw & 0xFu) << 3)) : 0;
+  }
+  // the V units at once
+  __device__ __forceinline__ void v_all() {
+#pragma unroll
+    for (int j = 0; j < kVUnits; ++j) {
+      v_unit(j);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) v_load(s);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) v_perm(s);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v_store(c);
+    }
   }
   // everything at once (the prologue's tiles)
   __device__ __forceinline__ void all() {
+    if constexpr (!Sh::kDirect) {
 #pragma unroll
-    for (int i = 0; i < kNK; ++i) k_load(i);
+      for (int i = 0; i < kNK; ++i) k_load(i);
 #pragma unroll
-    for (int i = 0; i < kNK; ++i) k_store(i);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) v_load(s);
+      for (int i = 0; i < kNK; ++i) k_store(i);
+    }
+    v_all();
     s_load();
-#pragma unroll
-    for (int s = 0; s < 4; ++s) v_perm(s);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) v_store(c);
     s_store();
   }
 };
 
+// The K operand of one QK step from a dword of packed int4 codes (8 channels, nibbles n0..n7): the bf16 integers
+// 128 + n in the order (n0, n4, n1, n5, n2, n6, n3, n7), as the K rows hold them.
+__device__ __forceinline__ bf16x8_t k_operand(uint32_t x) {
+  return as_bf16x8(u32x4_t{nib_pair(x), nib_pair(x >> 4), nib_pair(x >> 8), nib_pair(x >> 12)});
+}
+
 // Rows of the wide kernel per wave and per workgroup: NT 32-row tiles per wave.
 template <int HS>
-constexpr int wide_nt() { return HS >= 256 ? 1 : 2; }
+constexpr int wide_nt() { return HS >= 256 ? 1 : 2; }  // at head 512 the 32 rows' query operands take 128 VGPRs
 
 template <int HS, int NT>
 struct WRows {
@@ -178,10 +208,20 @@ struct WRows {
 };
 
 // S^T += K Q^T of one 16-channel step for the row tiles, as inline assembly writing VGPRs. `last` adds 24 wait states:
-// a 16-pass XDL result is complete before anything reads it.
-template <int NT>
+// a 16-pass XDL result is complete before anything reads it. WAIT puts 2 wait states before the MFMA, for a K operand
+// the VALU has just built (the compiler inserts them for its own MFMAs only).
+template <int NT, bool WAIT = false>
 __device__ __forceinline__ void wqk(f32x16_t (&s)[NT], bf16x8_t kop, const bf16x8_t (&q)[NT], bool first, bool last) {
-  if constexpr (NT == 1) {
+  if constexpr (WAIT) {
+    static_assert(NT == 1, "K operands built by the VALU: one row tile (head 512)");
+    if (first)
+      asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(s[0]) : "v"(kop), "v"(q[0]));
+    else if (last)
+      asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+                   : "+v"(s[0]) : "v"(kop), "v"(q[0]));
+    else
+      asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(s[0]) : "v"(kop), "v"(q[0]));
+  } else if constexpr (NT == 1) {
     if (first)
       asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(s[0]) : "v"(kop), "v"(q[0]));
     else if (last)
@@ -203,19 +243,19 @@ __device__ __forceinline__ void wqk(f32x16_t (&s)[NT], bf16x8_t kop, const bf16x
   }
 }
 
-// Softmax of one tile for the row tiles: scores from s (S^T), per-key scalars from the V buffer vb; P16 in PV operand
+// Softmax of one tile for the row tiles: scores from s (S^T), per-key scalars from the tile's scalar block sc; P16 in PV operand
 // order (pop[jt][ks]). Returns true when a score exceeds its row's maximum by more than the headroom (the row's
 // mnext then records the maximum to start again with; this tile's results are discarded).
 template <int HS, int KFMT, int NT, bool MASK>
-__device__ __forceinline__ bool w_softmax(WRows<HS, NT> &r, const f32x16_t (&s)[NT], const uint8_t *vb, int k0,
+__device__ __forceinline__ bool w_softmax(WRows<HS, NT> &r, const f32x16_t (&s)[NT], const uint8_t *sc, int k0,
                                           int kend, u32x4_t (&pop)[NT][2], int lane) {
   using Sh = WShape<HS, KFMT>;
   const int h = lane >> 5;
   float t[NT][16];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    const float4 a4 = *reinterpret_cast<const float4 *>(vb + Sh::kOffA + 4 * (8 * q + 4 * h));
-    const float4 e4 = *reinterpret_cast<const float4 *>(vb + Sh::kOffE + 4 * (8 * q + 4 * h));
+    const float4 a4 = *reinterpret_cast<const float4 *>(sc + Sh::kScA + 4 * (8 * q + 4 * h));
+    const float4 e4 = *reinterpret_cast<const float4 *>(sc + Sh::kScE + 4 * (8 * q + 4 * h));
     const float av[4] = {a4.x, a4.y, a4.z, a4.w}, ev[4] = {e4.x, e4.y, e4.z, e4.w};
 #pragma unroll
     for (int jt = 0; jt < NT; ++jt)
@@ -243,12 +283,12 @@ __device__ __forceinline__ bool w_softmax(WRows<HS, NT> &r, const f32x16_t (&s)[
       over = true;
     }
   }
-  const u32x4_t z0 = *reinterpret_cast<const u32x4_t *>(vb + Sh::kOffZ + 32 * h);
-  const u32x4_t z1 = *reinterpret_cast<const u32x4_t *>(vb + Sh::kOffZ + 32 * h + 16);
+  const u32x4_t z0 = *reinterpret_cast<const u32x4_t *>(sc + Sh::kScZ + 32 * h);
+  const u32x4_t z1 = *reinterpret_cast<const u32x4_t *>(sc + Sh::kScZ + 32 * h + 16);
   const uint32_t zp[8] = {z0[0], z0[1], z0[2], z0[3], z1[0], z1[1], z1[2], z1[3]};
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    const float4 s4 = *reinterpret_cast<const float4 *>(vb + Sh::kOffS + 4 * (8 * q + 4 * h));
+    const float4 s4 = *reinterpret_cast<const float4 *>(sc + Sh::kScS + 4 * (8 * q + 4 * h));
     const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
     for (int jt = 0; jt < NT; ++jt)
@@ -279,6 +319,12 @@ __device__ __forceinline__ void wpv_step(f32x16_t (&acc)[NT][CT], int ct, bf16x8
   else
     asm volatile("v_mfma_f32_32x32x16_bf16 %0, %2, %3, %0\n\tv_mfma_f32_32x32x16_bf16 %1, %2, %4, %1"
                  : "+a"(acc[0][ct]), "+a"(acc[1][ct]) : "v"(vop), "v"(p[0][ks]), "v"(p[1][ks]));
+}
+// Zeroes one accumulator tile with an MFMA on zero operands: as an assignment of zeros, the compiler kept one tile's
+// zeros in scratch across the restart loop at head 512 (all 256 AGPRs hold accumulators there). Only PV MFMAs, which
+// accumulate into it, read the tile next. The 2 wait states cover a zero operand the VALU has just written.
+__device__ __forceinline__ void wzero(f32x16_t &acc) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %1, 0" : "=a"(acc) : "v"(bf16x8_t{}));
 }
 // 24 wait states: the last inline 32x32x16 MFMA's result (16 passes) is complete before anything else touches it
 __device__ __forceinline__ void wpv_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
@@ -400,12 +446,12 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_wide_kernel(const Prefi
     const uint16_t *qr = p.qsigns ? nullptr : p.q + (int64_t)(q0 + tok) * p.qs0 + (int64_t)(kvh * G + jh) * p.qs1;
     const uint16_t *qs_row = qrot + (32 * jt + col) * HS;
     float qs = 0.f;  // the row's query sum: the 128 offset of the key operands (and the int4 zero point) folds into it
-    // the lane's channels: 16 cs + 8 h + e, e = 0..7, for cs = 0 .. HS / 16 - 1
+    // the lane's channels: step_chan(cs, h) + e, e = 0..7, for cs = 0 .. HS / 16 - 1
 #pragma unroll
     for (int cs = 0; cs < HS / 16; ++cs) {
       u32x4_t x;
-      if (p.qsigns) x = *reinterpret_cast<const u32x4_t *>(qs_row + 16 * cs + 8 * h);
-      else x = rv ? *reinterpret_cast<const u32x4_t *>(qr + 16 * cs + 8 * h) : u32x4_t{0u, 0u, 0u, 0u};
+      if (p.qsigns) x = *reinterpret_cast<const u32x4_t *>(qs_row + Sh::step_chan(cs, h));
+      else x = rv ? *reinterpret_cast<const u32x4_t *>(qr + Sh::step_chan(cs, h)) : u32x4_t{0u, 0u, 0u, 0u};
       qs += bf16_lo(x[0]) + bf16_hi(x[0]) + bf16_lo(x[1]) + bf16_hi(x[1]) + bf16_lo(x[2]) + bf16_hi(x[2]) +
             bf16_lo(x[3]) + bf16_hi(x[3]);
       if constexpr (KFMT == QP_CODES_INT4) {  // K operand order per 8 channels: (c0, c4, c1, c5, c2, c6, c3, c7)
@@ -430,11 +476,13 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_wide_kernel(const Prefi
   const int ntiles = ke > kb ? (ke - kb + kPfKeys - 1) / kPfKeys : 0;
   const int vis_all = first_pos + 1;  // keys below this are visible to every row of the block
 
-  auto pk_of = [&](int t) { return smem + (t % 3) * Pf::kPk; };
+  constexpr bool kDirect = Sh::kDirect;
+  auto pk_of = [&](int t) { return smem + (t % Sh::kSlots) * Sh::kSlot; };
   const uint32_t lds0 = uniform((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)smem);
-  auto pk_lds_of = [&](int t) { return lds0 + (uint32_t)((t % 3) * Pf::kPk); };
+  auto pk_lds_of = [&](int t) { return lds0 + (uint32_t)((t % Sh::kSlots) * Sh::kSlot); };
   auto kd_of = [&](int t) { return smem + Sh::kOffK + (t & 1) * Sh::kKd; };
-  auto vb_of = [&](int t) { return smem + Sh::kOffV + (t % 3) * Sh::kVb; };
+  auto vb_of = [&](int t) { return smem + Sh::kOffV + (t % Sh::kVbufs) * Sh::kVb; };
+  auto sc_of = [&](int t) { return kDirect ? smem + Sh::kOffR + (t & 1) * Sh::kSc : vb_of(t) + Sh::kVt; };
   auto tile_key = [&](int t) { return kb + t * kPfKeys; };
   const PfCopies<Pf> copies(w, lane);
   const uint8_t *hbase = p.kcodes + (int64_t)kvh * p.ks2;
@@ -450,17 +498,36 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_wide_kernel(const Prefi
       pf_gather<Pf>(p, trow, tile_key(t), ke, kvh, pk_of(t));
     }
   };
-  auto stager = [&](int t, bool full) {
+  // the unpack of tile tv's codes and tile ts's scalars (the same tile unless K direct)
+  auto stager = [&](int tv, int ts, bool full) {
     St st;
-    st.pk = pk_of(t);
-    st.kd = kd_of(t);
-    st.vt = vb_of(t);
+    st.pk = pk_of(tv);
+    st.kd = kd_of(tv);
+    st.vt = vb_of(tv);
+    st.pks = pk_of(ts);
+    st.sc = sc_of(ts);
     st.full = full;
-    st.k0 = tile_key(t);
+    st.k0 = tile_key(ts);
     st.kend = ke;
     st.tid = tid;
+    st.vu = tid & (HS - 1);
     st.scale_log2 = p.scale_log2;
     return st;
+  };
+  // S^T of tile t (K direct: lane half h reads code dwords 32 h + cs of key col, two steps per 8-byte read)
+  auto qk_tile = [&](f32x16_t (&sq)[NT], int t) {
+    const uint8_t *kp = pk_of(t) + col * Sh::kCell + (HS / 4) * h;
+    const uint8_t *kr = kd_of(t) + col * Sh::kKdRow + 16 * h;
+#pragma unroll
+    for (int cs = 0; cs < HS / 16; ++cs) {
+      bf16x8_t q[NT];
+#pragma unroll
+      for (int jt = 0; jt < NT; ++jt) q[jt] = r.qop[jt][cs];
+      bf16x8_t kop;
+      if constexpr (kDirect) kop = k_operand(reinterpret_cast<const u32x2_t *>(kp)[cs >> 1][cs & 1]);
+      else kop = *reinterpret_cast<const bf16x8_t *>(kr + 32 * cs);
+      wqk<NT, kDirect>(sq, kop, q, cs == 0, cs == HS / 16 - 1);
+    }
   };
   if (tid == 0) restart_word = 0;
 
@@ -471,9 +538,10 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_wide_kernel(const Prefi
       r.l[jt] = 0.f;
       r.c[jt] = 0.f;
 #pragma unroll
-      for (int ct = 0; ct < HS / 32; ++ct) r.acc[jt][ct] = f32x16_t{};
+      for (int ct = 0; ct < HS / 32; ++ct) wzero(r.acc[jt][ct]);
     }
-    // ---- prologue: tiles 0..2 fetched, 0 and 1 unpacked, tile 3 fetched, S(0), the first maximum, P(0)
+    // ---- prologue: tiles 0..2 fetched, 0 and 1 unpacked (K direct: tile 0, and tile 1's scalars), tile 3 fetched,
+    // S(0), the first maximum, P(0)
     fetch(0);
     if (ntiles > 1) fetch(1);
     if (ntiles > 2) fetch(2);
@@ -483,34 +551,33 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_wide_kernel(const Prefi
       else wait_vmcnt<0>();
     }
     __syncthreads();
-    stager(0, false).all();
+    stager(0, 0, false).all();
     if constexpr (SPAN) {
       if (ntiles > 2) copies.template wait<1>();
       else wait_vmcnt<0>();
     }
     __syncthreads();  // tile 0 unpacked; slot 0 free; tile 1 landed
     if (ntiles > 3) fetch(3);
-    if (ntiles > 1) stager(1, false).all();
-    f32x16_t s[NT];
-    {
-      const uint8_t *kr = kd_of(0) + col * Sh::kKdRow + 16 * h;
-#pragma unroll
-      for (int cs = 0; cs < HS / 16; ++cs) {
-        bf16x8_t q[NT];
-#pragma unroll
-        for (int jt = 0; jt < NT; ++jt) q[jt] = r.qop[jt][cs];
-        wqk<NT>(s, *reinterpret_cast<const bf16x8_t *>(kr + 32 * cs), q, cs == 0, cs == HS / 16 - 1);
+    if (ntiles > 1) {
+      St st = stager(1, 1, false);
+      if constexpr (kDirect) {
+        st.s_load();
+        st.s_store();
+      } else {
+        st.all();
       }
     }
+    f32x16_t s[NT];
+    qk_tile(s, 0);
     if (pass == 0) {  // the running maximum starts kWideBias above the first tile's row maximum
-      const uint8_t *vb = vb_of(0);
+      const uint8_t *sc = sc_of(0);
 #pragma unroll
       for (int jt = 0; jt < NT; ++jt) {
         float mx = -INFINITY;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const float4 a4 = *reinterpret_cast<const float4 *>(vb + Sh::kOffA + 4 * (8 * q + 4 * h));
-          const float4 e4 = *reinterpret_cast<const float4 *>(vb + Sh::kOffE + 4 * (8 * q + 4 * h));
+          const float4 a4 = *reinterpret_cast<const float4 *>(sc + Sh::kScA + 4 * (8 * q + 4 * h));
+          const float4 e4 = *reinterpret_cast<const float4 *>(sc + Sh::kScE + 4 * (8 * q + 4 * h));
           const float av[4] = {a4.x, a4.y, a4.z, a4.w}, ev[4] = {e4.x, e4.y, e4.z, e4.w};
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
@@ -525,7 +592,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_wide_kernel(const Prefi
       }
     }
     u32x4_t pop[NT][2];
-    if (w_softmax<HS, KFMT, NT, true>(r, s, vb_of(0), tile_key(0), ke, pop, lane)) restart_word = 1;
+    if (w_softmax<HS, KFMT, NT, true>(r, s, sc_of(0), tile_key(0), ke, pop, lane)) restart_word = 1;
 
     // block ids of tile 4 onwards, a tile ahead of their copies, through the scalar cache
     const __attribute__((address_space(4))) int32_t *ctab = (const __attribute__((address_space(4))) int32_t *)trow;
@@ -568,11 +635,39 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_wide_kernel(const Prefi
           fetch(it + 4);
         }
       }
-      // ---- phase A: S^T of tile it + 1 beside the unpack of tile it + 2 (past the last tiles: a stale slot into
-      // idle buffers, the same code path)
-      St st = stager(it + 2, kSteady);
+      // ---- phase A: S^T of tile it + 1 beside the unpack of tile it + 2 (K direct: tile it + 1's V and tile it + 2's
+      // scalars); past the last tiles a stale slot goes into idle buffers, the same code path
+      St st = kDirect ? stager(it + 1, it + 2, kSteady) : stager(it + 2, it + 2, kSteady);
       f32x16_t sn[NT];
-      {
+      if constexpr (kDirect) {
+        const uint8_t *kp = pk_of(it + 1) + col * Sh::kCell + (HS / 4) * h;
+        constexpr int kCs = HS / 16;
+        u32x2_t kraw[2];  // code dword pairs j (steps 2 j, 2 j + 1) at kraw[j & 1], read two pairs ahead
+        kraw[0] = *reinterpret_cast<const u32x2_t *>(kp);
+        kraw[1] = *reinterpret_cast<const u32x2_t *>(kp + 8);
+#pragma unroll
+        for (int cs = 0; cs < kCs; ++cs) {
+          const uint32_t x = kraw[(cs >> 1) & 1][cs & 1];
+          if ((cs & 1) && (cs >> 1) + 2 < kCs / 2)
+            kraw[(cs >> 1) & 1] = *reinterpret_cast<const u32x2_t *>(kp + 8 * ((cs >> 1) + 2));
+          bf16x8_t q[NT];
+#pragma unroll
+          for (int jt = 0; jt < NT; ++jt) q[jt] = r.qop[jt][cs];
+          wqk<NT, true>(sn, k_operand(x), q, cs == 0, cs == kCs - 1);
+          // the unpack, spread over the steps: the V units, then the scalars
+#pragma unroll
+          for (int j = 0; j < St::kVUnits; ++j) {
+            const int b = 2 + 8 * j;
+            if (cs == b) { st.v_unit(j); st.v_load(0); st.v_load(1); }
+            if (cs == b + 1) { st.v_load(2); st.v_load(3); }
+            if (cs == b + 2) { st.v_perm(0); st.v_perm(1); st.v_perm(2); st.v_perm(3); }
+            if (cs == b + 3) { st.v_store(0); st.v_store(1); }
+            if (cs == b + 4) { st.v_store(2); st.v_store(3); }
+          }
+          if (cs == 2 + 8 * St::kVUnits) st.s_load();
+          if (cs == 4 + 8 * St::kVUnits) st.s_store();
+        }
+      } else {
         const uint8_t *kr = kd_of(it + 1) + col * Sh::kKdRow + 16 * h;
         constexpr int kCs = HS / 16;
         constexpr int kLag = St::kNK < 4 ? St::kNK : 4;
@@ -617,7 +712,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_wide_kernel(const Prefi
             vbuf[sidx & 1] = *reinterpret_cast<const bf16x8_t *>(vr + 32 * Sh::kVtRow * nt + 32 * nk);
           }
           wpv_step<NT>(r.acc, ct, vop, pop, ks);
-          if (sidx == 1) over = w_softmax<HS, KFMT, NT, kMask>(r, sn, vb_of(it + 1), tile_key(it + 1), ke, pn, lane);
+          if (sidx == 1) over = w_softmax<HS, KFMT, NT, kMask>(r, sn, sc_of(it + 1), tile_key(it + 1), ke, pn, lane);
         }
       }
       if (__builtin_expect(over, 0)) restart_word = 1;
@@ -668,26 +763,29 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_wide_kernel(const Prefi
     const int rr = r0 + kRowsWave * w + 32 * jt + col;
     const int64_t tok = q0 + (valid ? rr / G : 0);
     const int64_t head = kvh * G + (valid ? rr % G : 0);
-    if (S == 1) {
-      const float inv = l > 0.f ? 1.f / l : 0.f;
-      uint16_t *orow = p.out + tok * p.os0 + head * p.os1;
-      float x[HS / 2];
-#pragma unroll
-      for (int ct = 0; ct < HS / 32; ++ct)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) x[16 * ct + i] = (r.acc[jt][ct][i] - csum) * inv;
-      if (p.osigns) w_rotate_out<HS>(x, p.osigns, p.out_scale, h);
-      if (valid) {
+    if constexpr (!kDirect) {  // K direct (head 512) always runs split (the merge rotates the 512-channel rows)
+      if (S == 1) {
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        uint16_t *orow = p.out + tok * p.os0 + head * p.os1;
+        float x[HS / 2];
 #pragma unroll
         for (int ct = 0; ct < HS / 32; ++ct)
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            *reinterpret_cast<u32x2_t *>(orow + 32 * ct + 8 * q + 4 * h) =
-                u32x2_t{pack_bf16x2(x[16 * ct + 4 * q], x[16 * ct + 4 * q + 1]),
-                        pack_bf16x2(x[16 * ct + 4 * q + 2], x[16 * ct + 4 * q + 3])};
+          for (int i = 0; i < 16; ++i) x[16 * ct + i] = (r.acc[jt][ct][i] - csum) * inv;
+        if (p.osigns) w_rotate_out<HS>(x, p.osigns, p.out_scale, h);
+        if (valid) {
+#pragma unroll
+          for (int ct = 0; ct < HS / 32; ++ct)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              *reinterpret_cast<u32x2_t *>(orow + 32 * ct + 8 * q + 4 * h) =
+                  u32x2_t{pack_bf16x2(x[16 * ct + 4 * q], x[16 * ct + 4 * q + 1]),
+                          pack_bf16x2(x[16 * ct + 4 * q + 2], x[16 * ct + 4 * q + 3])};
+        }
+        continue;
       }
-    } else {
-      if (!valid) continue;
+    }
+    if (valid) {
       float *orow = p.so + tok * p.sos0 + head * p.sos1 + (int64_t)split * HS;
 #pragma unroll
       for (int ct = 0; ct < HS / 32; ++ct)
@@ -718,7 +816,9 @@ int prefill_wide_rows(int head_size) {
 }
 
 void prefill_wide(const PrefillParams &p, int head_size, int key_format, dim3 grid, bool span, hipStream_t s) {
-  if (head_size == 256) {
+  if (head_size == 512) {
+    launch_wide<512, QP_CODES_INT4>(p, grid, span, s);  // int4 keys only (the router's choice)
+  } else if (head_size == 256) {
     if (key_format == QP_CODES_INT4) launch_wide<256, QP_CODES_INT4>(p, grid, span, s);
     else launch_wide<256, QP_CODES_INT8>(p, grid, span, s);
   } else {

@@ -13,7 +13,7 @@ import torch
 
 from .. import _hip
 
-MAX_HEAD = 256       # largest head size of the MFMA prefill kernel (head 512 prefills through split-KV query slices)
+MAX_HEAD = 512       # largest head size of the MFMA prefill kernels (head 512: the wide kernel with int4 keys)
 SEGMENT = 16384      # the reference's unpack segment; kept for callers that size bf16 scratch the same way
 MIN_QUERY = 64       # chunks at least this long take the prefill kernel even when they could take split-KV decode
 MIN_CONTEXT = 8192   # kept for API compatibility: the HIP prefill has no context threshold
@@ -57,9 +57,10 @@ def prefill_attention(q, k_cache, v_cache, k_scale_cache, v_scale_cache, out, *,
     When the chunk alone cannot fill the GPU, the keys are split over workgroups
     (num_splits, 0 = automatic) and merged; the fp32 partials go to a workspace from torch's caching allocator.
     max_seqlen_k bounds the automatic split count; without it the block table's capacity stands in (no host sync).
-    More than 12 query heads per KV head run the library's wide kernel (rows as (token, head) pairs on 32x32x16
-    MFMAs); head 512 runs the split-KV decode kernel over causal query slices of the chunk and merges (the library
-    picks the path)."""
+    More than 12 query heads per KV head, and head 512 with int4 keys, run the library's wide kernel (rows as
+    (token, head) pairs on 32x32x16 MFMAs; at head 512 always key-split, so it takes a workspace); head 512 with int8
+    keys runs the split-KV decode kernel over causal query slices of the chunk and merges (the library picks the
+    path)."""
     hs = q.shape[2]
     cache = _hip.paged_cache(k_cache, v_cache, k_scale_cache, v_scale_cache, hs)
     if max_seqlen_k is None:
