@@ -373,6 +373,19 @@ def test_decode_head_512(device, fmt, T):
     assert O.relerr(out, ref) < 5e-3
 
 
+@pytest.mark.parametrize("T", [1, 2])
+def test_decode_head_512_row_loader(device, T):
+    """Head 512 int4 cache stored NHD (slots of one head strided by the KV heads): the generic strided-row kernel,
+    whose scale words are read through one lane-chosen pointer, against the same cells stored HND."""
+    a, emu, ref, _ = _decode_case(device, np.random.default_rng(310 + T), "int4", [(T, 2500), (1, 700)], nq=16, nkv=2,
+                                  hs=512, segments=5)
+    b, _, _, _ = _decode_case(device, np.random.default_rng(310 + T), "int4", [(T, 2500), (1, 700)], nq=16, nkv=2,
+                              hs=512, segments=5, layout="nhd")
+    assert_emulation(b, emu)
+    assert O.relerr(b, ref) < 5e-3
+    assert O.relerr(a, b) < 5e-3
+
+
 @pytest.mark.parametrize("fmt", ["int4", "int8"])
 def test_decode_gqa_8_and_head_128(device, fmt):
     """Head 128, 8 query heads per KV head: 4 tokens are two row tiles (AGPR accumulators), 1 token one row tile
@@ -784,6 +797,36 @@ def test_prefill_wide_table_row_exactly_as_long_as_the_context(device, fmt, n, h
     out, emu, ref = _prefill_case(device, rng, fmt, [(20, n)], nq=16, nkv=1, hs=hs)
     assert_emulation(out, emu)
     assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
+
+
+@pytest.mark.parametrize("hs", [256, 512])
+def test_prefill_wide_rows_without_keys_are_zero(device, hs):
+    """A sequence whose context holds no keys (seqused_k = 0 beside a query chunk; vLLM does not send these) leaves
+    the wide kernel's row blocks without a tile: its rows come out zero, with one split (the epilogue's normalisation
+    of empty accumulators) and with several (every split empty for the merge), and the other sequence is unaffected."""
+    import torch
+
+    from vllm_quantpack.attention import int4_prefill
+    rng = np.random.default_rng(285 + hs)
+    bs, nq, nkv, n = 16, 16, 1, 700
+    nb = -(-n // bs)
+    kv, v = random_cache(rng, nb + 1, nkv, bs, hs)
+    _, (kc, vc, ks, vs) = torch_cache(kv, hs, "int4", device)
+    table = np.zeros((2, nb), np.int32)
+    table[0] = np.arange(nb)
+    q = O.f32_to_bf16_bits(rng.standard_normal((13, nq, hs)).astype(np.float32))
+    qt = bf16_tensor(q, device)
+    scale = hs ** -0.5
+    for splits in (1, 3):
+        out = torch.full_like(qt, float("nan"))
+        int4_prefill.prefill_attention(qt, kc, vc, ks, vs, out, cu_seqlens_q=i32([0, 8, 13], device),
+                                       seqused_k=i32([n, 0], device), block_table=i32(table, device), max_seqlen_q=8,
+                                       softmax_scale=scale, num_splits=splits)
+        torch.cuda.synchronize()
+        got = to_f32(out)
+        assert np.all(got[8:] == 0), splits
+        emu = O.decode_emulated(O.bf16_bits_to_f32(q)[:8], v, table[0], n, scale, num_segments=1, tile=64)
+        assert_emulation(got[:8], emu, splits)
 
 
 @pytest.mark.parametrize("fmt,hs", [("int4", 256), ("int8", 256), ("int4", 512)])

@@ -27,6 +27,11 @@
 // walk of PfCopies / kPfSteadyLead), all 256 threads unpack tile i + 2 to exact bf16 integers (K rows 128 + n, V^T rows
 // 16 + n, per-key scalars) while the waves run S^T of tile i + 1, then O^T += V^T P^T of tile i runs beside the softmax
 // of tile i + 1.
+// Head 512 (int4 keys; one 32-row tile per wave: 128 VGPRs of query operands, all 256 AGPRs of accumulators): two bf16
+// K buffers would not fit beside the V^T buffers in the 160 KB, so each wave builds its K operands from the packed codes
+// in LDS (one 8-byte read per two steps, four v_bitop3 per step, as the unpack would), V^T is unpacked one tile ahead
+// into two buffers and the per-key scalars two tiles ahead into a ring of two: 4 packed slots + 2 V^T buffers + the
+// ring = 146 KB. That kernel always runs key-split: the merge normalises and rotates its 512-channel rows.
 // The running maximum m of a row starts kWideBias log2 units above the first tile's maximum, and probabilities are
 // taken as 2^(s - m) as long as no score exceeds m by more than kWideHeadroom (fp32 then holds l, the zero-point sum and
 // the accumulators over 2^17 keys: below 2^122). A score beyond (136 units above the first tile's maximum; never seen
@@ -469,6 +474,8 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_wide_kernel(const Prefi
     r.qsum[jt] = qs;
     r.m[jt] = -INFINITY;
     r.mnext[jt] = -INFINITY;
+    r.l[jt] = 0.f;  // (a split without tiles keeps these: its rows are written as empty)
+    r.c[jt] = 0.f;
   }
   if (p.qsigns) __syncthreads();  // every wave holds its operands: the rotated rows' LDS is free for the copies
 
@@ -768,10 +775,12 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_wide_kernel(const Prefi
         const float inv = l > 0.f ? 1.f / l : 0.f;
         uint16_t *orow = p.out + tok * p.os0 + head * p.os1;
         float x[HS / 2];
+        // (l = 0: a row block without keys in its split, whose accumulators were never zeroed; the merge skips the
+        // partials of such blocks by their m = -inf, the only thing it reads of them)
 #pragma unroll
         for (int ct = 0; ct < HS / 32; ++ct)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) x[16 * ct + i] = (r.acc[jt][ct][i] - csum) * inv;
+          for (int i = 0; i < 16; ++i) x[16 * ct + i] = l > 0.f ? (r.acc[jt][ct][i] - csum) * inv : 0.f;
         if (p.osigns) w_rotate_out<HS>(x, p.osigns, p.out_scale, h);
         if (valid) {
 #pragma unroll
