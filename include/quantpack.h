@@ -51,7 +51,7 @@ typedef struct qp_paged_cache {
   int32_t num_blocks;
   int32_t block_size;
   int32_t num_kv_heads;
-  int32_t head_size;
+  int32_t head_size; /* 64, 128, 256 or 512 for store, decode, prefill and the router (unpack: any multiple of 8) */
 } qp_paged_cache;
 
 /*
@@ -135,8 +135,8 @@ int qp_merge_segments(const qp_merge_args *args, qp_stream_t stream);
  * (num_splits, 0 = chosen for the device) whose fp32 partials go to the caller's workspace and are merged as in
  * qp_merge_segments; without enough workspace an automatic choice falls back to one split.
  * More than 12 query heads per KV head run a wide variant whose 32-row MFMA tiles hold (token, head) pairs. Head 512
- * with int4 keys runs that variant too, always with at least 2 splits; with int8 keys it runs the split-KV decode
- * kernel over causal query slices of at most 4 tokens and merges. Both head-512 paths need the workspace
+ * with int4 keys runs that variant too, always with at least 2 splits; with int8 keys, and head 64, it runs the
+ * split-KV decode kernel over causal query slices of at most 4 tokens and merges. These paths need the workspace
  * (qp_prefill_workspace_size bytes, 256-byte aligned).
  * With rht_signs the result is rotated back, out = (o H D) * rht_out_scale, as qp_merge_segments does.
  * Replaces prefill_sequence (int4_prefill.py:203-232: unpack to bf16 segments + FlashAttention + LSE merge, with the

@@ -373,6 +373,18 @@ def test_decode_head_512(device, fmt, T):
     assert O.relerr(out, ref) < 5e-3
 
 
+@pytest.mark.parametrize("fmt,T,layout", [("int4", 1, "hnd"), ("int4", 2, "nhd"), ("int4", 3, "hnd"),
+                                           ("int4", 4, "hnd"), ("int8", 1, "hnd"), ("int8", 4, "nhd")])
+def test_decode_head_64(device, fmt, T, layout):
+    """Head 64 (Llama 3.2 1B-class models: 8 query heads per KV head): 72-byte int4 and 104-byte k8v4 cells, one
+    channel block of PV, two row tiles at 4 tokens; both loaders."""
+    rng = np.random.default_rng(320 + T + (10 if fmt == "int8" else 0))
+    out, emu, ref, _ = _decode_case(device, rng, fmt, [(T, 3000), (1, 900), (2, 17)], nq=16, nkv=2, hs=64,
+                                    segments=6, layout=layout)
+    assert_emulation(out, emu)
+    assert O.relerr(out, ref) < 5e-3
+
+
 @pytest.mark.parametrize("T", [1, 2])
 def test_decode_head_512_row_loader(device, T):
     """Head 512 int4 cache stored NHD (slots of one head strided by the KV heads): the generic strided-row kernel,
@@ -400,10 +412,13 @@ def test_decode_gqa_8_and_head_128(device, fmt):
 
 @pytest.mark.parametrize("fmt", ["int4", "int8"])
 @pytest.mark.parametrize("layout", ["hnd", "nhd"])
-def test_store_bit_exact(device, fmt, layout):
+@pytest.mark.parametrize("hs", [256, 64])
+def test_store_bit_exact(device, fmt, layout, hs):
+    """Bit-exact stores; head 64 holds one channel per lane, so each int4 byte joins two lanes."""
     import torch
 
     from vllm_quantpack.attention import k8v4_kv
+    HS = hs
     rng = np.random.default_rng(61)
     nb, bs, n = 20, 16, 200
     kv_np = O.new_cache(nb, NKV, bs, O.int4_cell_bytes(HS) if fmt == "int4" else O.k8v4_cell_bytes(HS), layout)
@@ -761,6 +776,16 @@ def test_prefill_head_512(device, fmt):
     tests/test_int4_kv.py:194-210, tests/test_k8v4_kv.py:208-225). Ragged batch."""
     rng = np.random.default_rng(401 + (1 if fmt == "int8" else 0))
     out, emu, ref = _prefill_case(device, rng, fmt, [(37, 2100), (5, 600), (1, 64)], nq=16, nkv=2, hs=512)
+    assert_emulation(out, emu)
+    assert O.relerr(out, ref) < 5e-3
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+def test_prefill_head_64(device, fmt):
+    """Head 64 prefills over causal query slices of the split-KV kernel (the reference's kernels take any head size:
+    int4_kv.py:130-131). Ragged batch, with a first chunk (context == chunk)."""
+    rng = np.random.default_rng(407 + (1 if fmt == "int8" else 0))
+    out, emu, ref = _prefill_case(device, rng, fmt, [(37, 2100), (20, 20), (1, 64)], nq=16, nkv=2, hs=64)
     assert_emulation(out, emu)
     assert O.relerr(out, ref) < 5e-3
 

@@ -112,6 +112,24 @@ def test_mixed_batch_long_prefill_and_mtp_decodes(device, fmt):
     assert np.isfinite(to_f32(segm[1])[:8, :, 0]).all() and np.isnan(to_f32(segm[1])[8:]).all()
 
 
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+def test_mixed_batch_head_64(device, fmt):
+    """Head 64 through the drop-in: a 40-token chunk (query slices of the split-KV kernel) beside decodes of 4 and 1
+    tokens, the rotations fused, 16 query heads on 2 KV heads; within 0.5 % of fp64."""
+    import torch
+    seqs = [(40, 3000), (4, 2000), (1, 700)]
+    views, table, q, cu, lens, qlens, ref = _batch(device, seqs, fmt, 520 + (fmt == "int8"), nkv=2, hs=64, nq=16)
+    out = torch.full_like(q, float("nan"))
+    segm = _segm(device, 32, 16, nq=16, hs=64)
+    _call(views, q, out, i32(cu, device), i32(lens, device), i32(table, device), max(qlens), max(lens), segm, 16,
+          hs=64)
+    torch.cuda.synchronize()
+    got = to_f32(out)
+    for i in range(len(seqs)):
+        sl = slice(cu[i], cu[i + 1])
+        assert O.relerr(got[sl], ref[sl]) < 5e-3, (i, O.relerr(got[sl], ref[sl]))
+
+
 def test_mixed_batch_short_rows_beyond_the_segment_buffers(device):
     """Segment buffers of 5 rows take the first two short sequences (4 + 1 rows); the next short sequence no longer
     fits and the prefill kernel serves it, as it does the chunk. Ragged lengths, first chunk without cached keys."""

@@ -81,7 +81,8 @@ AttentionPlan plan_attention(const qp_paged_cache *cache, const qp_attention_arg
   const int hs = cache->head_size;
   const int G = cache->num_kv_heads > 0 ? a->num_q_heads / cache->num_kv_heads : 0;
   const bool segm = a->segm_output && a->segm_max && a->segm_expsum && a->segm_rows > 0 && a->num_segments >= 1;
-  const bool decode_shape = segm && (hs == 128 || hs == 256 || hs == 512) && G >= 1 && G <= 32 && (hs != 512 || G <= 16);
+  const bool decode_shape =
+      segm && (hs == 64 || hs == 128 || hs == 256 || hs == 512) && G >= 1 && G <= 32 && (hs != 512 || G <= 16);
   P.plain_decode = decode_shape && a->max_query_len >= 1 && a->max_query_len <= QP_DECODE_MAX_QUERY &&
                    a->max_query_len * G <= 32 && a->num_tokens <= a->segm_rows;
   P.routed = decode_shape && !P.plain_decode;
@@ -276,7 +277,8 @@ extern "C" int qp_attention_noalloc(const qp_paged_cache *cache, const qp_attent
                    args->max_query_len * G <= 32,
                "qp_attention_noalloc: only batches of sequences with 1..4 query tokens and at most 32 query rows per "
                "KV head (a decode step)");
-  QP_SUPPORTED(hs == 128 || hs == 256 || hs == 512, "qp_attention_noalloc: head size must be 128, 256 or 512");
+  QP_SUPPORTED(hs == 64 || hs == 128 || hs == 256 || hs == 512,
+               "qp_attention_noalloc: head size must be 64, 128, 256 or 512");
   QP_SUPPORTED(hs != 512 || G <= 16, "qp_attention_noalloc: head 512 takes at most 16 query heads per KV head");
   QP_REQUIRE(args->num_segments >= 1 && args->num_segments <= 2048, "qp_attention_noalloc: 1..2048 segments");
   // [segment rows: tokens x heads x segments x head_size | maxima | sums], fp32, each part 256-byte aligned

@@ -153,15 +153,17 @@ struct WaveState {
 };
 
 // The workgroup's query rows rotated once, for every wave to read: row r (< T G, the rest zero) by wave r % WAVES with
-// all 64 lanes (HS / 64 channels per lane), x D then H in the channel-bit order of rht_kernel and load_query_row, so
-// the bf16 rows are bit-identical to theirs. Each wave rotating all rows itself (about 900 instructions per lane at
-// head 256, before its first copy could issue) cost 3 us of a 131072-key decode.
+// all 64 lanes (HS / 64 channels per lane; 32 lanes of 2 at head 64), x D then H in the channel-bit order of rht_kernel
+// and load_query_row, so the bf16 rows are bit-identical to theirs. Each wave rotating all rows itself (about 900
+// instructions per lane at head 256, before its first copy could issue) cost 3 us of a 131072-key decode.
 template <int HS, int NCT, int WAVES>
 __device__ __forceinline__ void rotate_rows_shared(uint16_t *qrot, const DecodeParams &p, int q0, int T, int h, int G,
                                                    int w, int lane) {
-  constexpr int CPL = HS / 64;
+  constexpr int CPL = HS >= 128 ? HS / 64 : 2;  // channels per lane
+  constexpr int LANES = HS / CPL;               // lanes holding a row
   static_assert(CPL == 2 || CPL == 4 || CPL == 8 || CPL == 16, "head size");
   const int R = T * G;
+  if (lane >= LANES) return;  // (head 64: lanes 32..63 hold nothing; the butterflies stay in lanes 0..31)
   for (int r = w; r < NCT * 16; r += WAVES) {
     uint32_t *dst = reinterpret_cast<uint32_t *>(qrot + r * HS + CPL * lane);
     if (r < R) {
@@ -175,7 +177,7 @@ __device__ __forceinline__ void rotate_rows_shared(uint16_t *qrot, const DecodeP
         x[2 * i] = bf16_lo(v) * p.qsigns[CPL * lane + 2 * i];
         x[2 * i + 1] = bf16_hi(v) * p.qsigns[CPL * lane + 2 * i + 1];
       }
-      fwht_lanes<CPL>(x, lane);
+      fwht_lanes<CPL, LANES>(x, lane);
 #pragma unroll
       for (int i = 0; i < CPL / 2; ++i) dst[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
     } else {
@@ -1508,7 +1510,8 @@ int check_decode(const qp_paged_cache *cache, const qp_decode_args *a, bool rout
                  a->segm_expsum,
              "qp_decode_splitkv: null tensor");
   const int hs = cache->head_size;
-  QP_SUPPORTED(hs == 128 || hs == 256 || hs == 512, "qp_decode_splitkv: head size must be 128, 256 or 512");
+  QP_SUPPORTED(hs == 64 || hs == 128 || hs == 256 || hs == 512,
+               "qp_decode_splitkv: head size must be 64, 128, 256 or 512");
   QP_REQUIRE(cache->key.format == QP_CODES_INT4 || cache->key.format == QP_CODES_INT8,
              "qp_decode_splitkv: unknown key format");
   QP_REQUIRE(cache->value.format == QP_CODES_INT4, "qp_decode_splitkv: values must be int4");
@@ -1730,6 +1733,7 @@ int dispatch_hs(const qp_paged_cache *cache, const DecodeParams &p, int nct, dim
   QP_SUPPORTED(span || hs != 512 || cache->key.format == QP_CODES_INT4,
                "head 512 with int8 keys needs the standard cell layout");
   if (hs == 512) return dispatch_decode<512>(p, cache->key.format, nct, grid, span, s);
+  if (hs == 64) return dispatch_decode<64>(p, cache->key.format, nct, grid, span, s);
   if (hs == 256) return dispatch_decode<256>(p, cache->key.format, nct, grid, span, s);
   return dispatch_decode<128>(p, cache->key.format, nct, grid, span, s);
 }

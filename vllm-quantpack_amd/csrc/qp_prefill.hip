@@ -823,7 +823,8 @@ void dispatch_nt(const PrefillParams &p, int nt, dim3 grid, bool span, hipStream
 // Which kernel serves a prefill: the 16-row-tile kernel above up to 12 query heads per KV head; the wide kernel
 // (qp_prefill_wide.hip: 128 or 256 (token, head) rows per workgroup on 32x32x16 MFMAs, any GQA width) above that and
 // for head 512 with int4 keys; the query-slice path for head 512 with int8 keys, whose 776-byte cells do not fit the
-// wide kernel's LDS plan. (At head 256 the wide kernel holds one 32-row tile per wave, so each K / V operand it reads
+// wide kernel's LDS plan, and for head 64, whose 4 QK steps per tile leave the MFMA kernels' unpack nothing to hide
+// behind. (At head 256 the wide kernel holds one 32-row tile per wave, so each K / V operand it reads
 // from LDS serves 32 rows against the tile kernel's 48: 6.3 against 3.3 ms on the 1024-token chunk over 131072 keys
 // with 6 query heads per KV head.)
 enum class PrefillPath { kSlices, kTiles, kWide };
@@ -882,7 +883,7 @@ int prefill_run(const qp_paged_cache *cache, const qp_prefill_args *a, const int
              "qp_prefill: null cache view");
   QP_REQUIRE(a->query && a->cu_seqlens_q && a->seqused_k && a->block_table && a->out, "qp_prefill: null tensor");
   const int hs = cache->head_size;
-  QP_SUPPORTED(hs == 128 || hs == 256 || hs == 512, "qp_prefill: head size must be 128, 256 or 512");
+  QP_SUPPORTED(hs == 64 || hs == 128 || hs == 256 || hs == 512, "qp_prefill: head size must be 64, 128, 256 or 512");
   QP_REQUIRE(cache->key.format == QP_CODES_INT4 || cache->key.format == QP_CODES_INT8, "qp_prefill: bad key format");
   QP_REQUIRE(cache->value.format == QP_CODES_INT4, "qp_prefill: values must be int4");
   QP_REQUIRE(cache->num_kv_heads > 0 && a->num_q_heads > 0 && a->num_q_heads % cache->num_kv_heads == 0,

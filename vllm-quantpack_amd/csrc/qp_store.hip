@@ -74,15 +74,22 @@ __device__ __forceinline__ uint32_t quant_int4(const float (&x)[E], uint8_t *cod
   const float scale = fmaxf((hi - lo) / 15.0f, 1e-6f);
   const float zp = fminf(fmaxf(round_half_away(-lo / scale), 0.f), 15.f);
   const float inv = 1.0f / scale;
-  uint8_t b[E / 2];
+  if constexpr (E == 1) {
+    // head 64, one channel per lane: the byte of channels 2i and 2i + 1 joins lanes 2i and 2i + 1
+    const uint32_t q = (uint32_t)fminf(fmaxf(round_half_away(fmaf(x[0], inv, zp)), 0.f), 15.f);
+    const uint32_t qn = (uint32_t)__shfl_xor((int)q, 1, 64);
+    if (!(lane & 1)) codes_row[lane >> 1] = (uint8_t)((q & 0xF) | ((qn & 0xF) << 4));
+  } else {
+    uint8_t b[E / 2];
 #pragma unroll
-  for (int i = 0; i < E; i += 2) {
-    const uint32_t q0 = (uint32_t)fminf(fmaxf(round_half_away(fmaf(x[i], inv, zp)), 0.f), 15.f);
-    const uint32_t q1 = (uint32_t)fminf(fmaxf(round_half_away(fmaf(x[i + 1], inv, zp)), 0.f), 15.f);
-    b[i / 2] = (uint8_t)((q0 & 0xF) | ((q1 & 0xF) << 4));
+    for (int i = 0; i < E; i += 2) {
+      const uint32_t q0 = (uint32_t)fminf(fmaxf(round_half_away(fmaf(x[i], inv, zp)), 0.f), 15.f);
+      const uint32_t q1 = (uint32_t)fminf(fmaxf(round_half_away(fmaf(x[i + 1], inv, zp)), 0.f), 15.f);
+      b[i / 2] = (uint8_t)((q0 & 0xF) | ((q1 & 0xF) << 4));
+    }
+#pragma unroll
+    for (int i = 0; i < E / 2; ++i) codes_row[lane * (E / 2) + i] = b[i];
   }
-#pragma unroll
-  for (int i = 0; i < E / 2; ++i) codes_row[lane * (E / 2) + i] = b[i];
   return (__float_as_uint(scale) & 0xFFFFFFF0u) | (uint32_t)zp;
 }
 
@@ -186,7 +193,7 @@ extern "C" int qp_store(const qp_paged_cache *cache, const qp_store_args *a, qp_
   QP_REQUIRE(cache->key.codes && cache->key.words && cache->value.codes && cache->value.words,
              "qp_store: null cache view");
   const int hs = cache->head_size;
-  QP_SUPPORTED(hs == 128 || hs == 256 || hs == 512, "qp_store: head size must be 128, 256 or 512");
+  QP_SUPPORTED(hs == 64 || hs == 128 || hs == 256 || hs == 512, "qp_store: head size must be 64, 128, 256 or 512");
   QP_REQUIRE(cache->key.format == QP_CODES_INT4 || cache->key.format == QP_CODES_INT8, "qp_store: bad key format");
   QP_REQUIRE(cache->value.format == QP_CODES_INT4, "qp_store: values must be int4");
   QP_REQUIRE(cache->block_size > 0 && cache->num_kv_heads > 0 && a->num_tokens >= 0, "qp_store: bad sizes");
@@ -221,6 +228,7 @@ extern "C" int qp_store(const qp_paged_cache *cache, const qp_store_args *a, qp_
   const dim3 grid(a->num_tokens, cache->num_kv_heads);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (hs) {
+    case 64: launch_store<1>(p, cache->key.format, grid, s); break;
     case 128: launch_store<2>(p, cache->key.format, grid, s); break;
     case 256: launch_store<4>(p, cache->key.format, grid, s); break;
     default: launch_store<8>(p, cache->key.format, grid, s); break;
