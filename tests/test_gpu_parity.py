@@ -790,6 +790,19 @@ def test_prefill_head_64(device, fmt):
     assert O.relerr(out, ref) < 5e-3
 
 
+@pytest.mark.parametrize("nq,nkv,hs", [(12, 4, 256), (20, 4, 256), (28, 4, 128), (32, 4, 256), (32, 2, 256),
+                                       (16, 4, 128)])
+def test_prefill_tile_rows_at_any_gqa_width(device, nq, nkv, hs):
+    """The tile kernel's 192-row blocks of (token, query head) pairs at GQA 3, 5, 7, 8 and 16 (and 4 at head 128): a
+    ragged batch whose blocks straddle tokens and sequences end mid-block, against the emulation and fp64."""
+    rng = np.random.default_rng(410 + nq + hs)
+    lens = [(70, 2500), (5, 900), (1, 1), (33, 33), (17, 64)]
+    out, emu, ref = _prefill_case(device, rng, "int4", lens, nq=nq, nkv=nkv, hs=hs)
+    assert np.isfinite(out).all()
+    assert_emulation(out, emu)
+    assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
+
+
 def test_prefill_wide_gqa(device):
     """16 query heads per KV head is past the 16-row-tile kernel's 12: the wide kernel (32x32x16 MFMAs, rows as
     (token, head) pairs) serves it."""
@@ -802,10 +815,10 @@ def test_prefill_wide_gqa(device):
 @pytest.mark.parametrize("fmt", ["int4", "int8"])
 @pytest.mark.parametrize("hs,splits", [(256, 1), (256, 3), (128, 1), (128, 2), (512, 1), (512, 3)])
 def test_prefill_wide_kernel_batches(device, fmt, hs, splits):
-    """The wide kernel on a batch whose row blocks (128 rows at heads 256 and 512, 256 at head 128) straddle tokens
-    and end mid-block: a long chunk, a first chunk (context == chunk), a single token, a 130-token chunk; 32 query heads
-    on 2 KV heads; with key splits, some of them empty (head 512 runs at least 2; with int8 keys it takes the query
-    slices)."""
+    """16 query heads per KV head on a batch whose row blocks (256 rows at head 128 and 128 at head 512 on the wide
+    kernel, 192 at head 256 on the tile kernel) straddle tokens and end mid-block: a long chunk, a first chunk (context
+    == chunk), a single token, a 130-token chunk; 32 query heads on 2 KV heads; with key splits, some of them empty
+    (head 512 runs at least 2; with int8 keys it takes the query slices)."""
     rng = np.random.default_rng(260 + hs + splits + (1 if fmt == "int8" else 0))
     lens = [(40, 3000), (7, 7), (1, 500), (130, 900)]
     out, emu, ref = _prefill_case(device, rng, fmt, lens, nq=32, nkv=2, hs=hs, splits=splits)
@@ -814,7 +827,7 @@ def test_prefill_wide_kernel_batches(device, fmt, hs, splits):
     assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
 
 
-@pytest.mark.parametrize("fmt,n,hs", [("int4", 330, 256), ("int8", 1000, 256), ("int4", 1009, 512), ("int4", 353, 512)])
+@pytest.mark.parametrize("fmt,n,hs", [("int4", 330, 128), ("int8", 1000, 128), ("int4", 1009, 512), ("int4", 353, 512)])
 def test_prefill_wide_table_row_exactly_as_long_as_the_context(device, fmt, n, hs):
     """One sequence whose block table holds exactly ceil(n / 16) entries and whose last tile has 1..16 keys, on the
     wide kernel (the CPU walk in test_prefill_table_walk checks its table reads)."""
@@ -824,11 +837,12 @@ def test_prefill_wide_table_row_exactly_as_long_as_the_context(device, fmt, n, h
     assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
 
 
-@pytest.mark.parametrize("hs", [256, 512])
+@pytest.mark.parametrize("hs", [128, 256, 512])
 def test_prefill_wide_rows_without_keys_are_zero(device, hs):
     """A sequence whose context holds no keys (seqused_k = 0 beside a query chunk; vLLM does not send these) leaves
-    the wide kernel's row blocks without a tile: its rows come out zero, with one split (the epilogue's normalisation
-    of empty accumulators) and with several (every split empty for the merge), and the other sequence is unaffected."""
+    the row blocks without a tile (the wide kernel at heads 128 and 512, the tile kernel at 256): its rows come out
+    zero, with one split (the epilogue's normalisation of empty accumulators) and with several (every split empty for
+    the merge), and the other sequence is unaffected."""
     import torch
 
     from vllm_quantpack.attention import int4_prefill
@@ -854,7 +868,7 @@ def test_prefill_wide_rows_without_keys_are_zero(device, hs):
         assert_emulation(got[:8], emu, splits)
 
 
-@pytest.mark.parametrize("fmt,hs", [("int4", 256), ("int8", 256), ("int4", 512)])
+@pytest.mark.parametrize("fmt,hs", [("int4", 128), ("int8", 128), ("int4", 512)])
 def test_prefill_wide_scores_far_above_the_first_tile(device, fmt, hs):
     """Key scales of 2^7 .. 2^12 late in the context put scores thousands of log2 units above the first tile's
     maximum, past the wide kernel's headroom: the workgroup runs its split again with the raised maxima (once per
@@ -867,7 +881,7 @@ def test_prefill_wide_scores_far_above_the_first_tile(device, fmt, hs):
     assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
 
 
-@pytest.mark.parametrize("hs", [256, 512])
+@pytest.mark.parametrize("hs", [128, 512])
 def test_prefill_wide_fused_rotations(device, hs):
     """On the wide kernel: the query rotated on load gives the bits of rotating it first, and the output rotated back
     in the epilogue (one split) or by the merge (three; at head 512 the kernel always splits) matches a separate
@@ -900,11 +914,11 @@ def test_prefill_wide_fused_rotations(device, hs):
         assert O.relerr(to_f32(got), want) < 1e-2, splits
 
 
-@pytest.mark.parametrize("fmt,hs,nq", [("int8", 256, NQ), ("int4", 512, 16)])
+@pytest.mark.parametrize("fmt,hs,nq", [("int8", 256, NQ), ("int4", 512, 16), ("int8", 128, 16)])
 def test_prefill_span_and_row_loaders_agree(device, fmt, hs, nq):
-    """The page-run copies (HND) and the strided gather (NHD) of the prefill kernel (and at head 512 the wide one) on
-    the same cache contents."""
-    case = dict(hs=hs, nq=nq, nkv=2 if hs == 512 else NKV)
+    """The page-run copies (HND) and the strided gather (NHD) of the tile kernel (head 256) and the wide one (head 128
+    with 8 query heads per KV head, head 512) on the same cache contents."""
+    case = dict(hs=hs, nq=nq, nkv=2 if hs in (128, 512) else NKV)
     a, emu, ref = _prefill_case(device, np.random.default_rng(204), fmt, [(64, 1500), (3, 700)], **case)
     b, _, _ = _prefill_case(device, np.random.default_rng(204), fmt, [(64, 1500), (3, 700)], layout="nhd", **case)
     assert_emulation(a, emu)

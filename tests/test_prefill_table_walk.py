@@ -5,7 +5,8 @@ t + 5 one iteration ahead of its copies, through a pointer that steps two entrie
 (the tile kernel's six-phase unrolled loop of int4 keys and rolled steady loop of int8 keys, the wide kernel's steady
 loop) take the pair's second entry without checking the split's end, which is only valid when that tile is followed by
 another one. This walk restates each kernel's loop structure (prologue and loops, with the `kPfSteadyLead` bound read
-from the source) and checks, for every context length mod 32 and the key-split geometry the kernels use, that
+from the source) and checks, for every context length mod 32, row blocks of (token, head) pairs at several GQA widths
+and the key-split geometry the kernels use, that
 
 * every entry read lies inside the sequence's own row (index < ceil(kend / 16)), so a table whose row holds exactly
   ceil(n / 16) entries is never read past its end;
@@ -33,13 +34,13 @@ def steady_lead() -> int:
     return int(m.group(1))
 
 
-def walk(n, qlen, t0, bq, split, splits, int4, lead, wide=False):
-    """Table indices read by one workgroup (query block at local token t0 of a qlen-token chunk whose last token sees
-    n keys; key split `split` of `splits`), as the kernel reads them (wide: prefill_wide_kernel's loops, whose
-    iterations run up to the split's second-to-last tile). Returns (reads, expected) lists of (tile, index)."""
-    ntok = min(bq, qlen - t0)
-    first_pos = n - qlen + t0
-    kend = max(0, min(n, first_pos + ntok))
+def walk(n, qlen, t_first, t_last, split, splits, int4, lead, wide=False):
+    """Table indices read by one workgroup (a row block whose (token, head) rows span local tokens t_first..t_last of
+    a qlen-token chunk whose last token sees n keys; key split `split` of `splits`), as the kernel reads them (wide:
+    prefill_wide_kernel's loops, whose iterations run up to the split's second-to-last tile). Returns (reads,
+    expected) lists of (tile, index)."""
+    first_pos = n - qlen + t_first
+    kend = max(0, min(n, n - qlen + t_last + 1))
     seg = -(-n // (splits * DECODE_TILE)) * DECODE_TILE
     kb = split * seg
     ke = min(kend, kb + seg)
@@ -109,19 +110,26 @@ def shapes():
                         yield n, qlen, splits
 
 
-KERNELS = [dict(int4=True), dict(int4=False), dict(int4=True, wide=True)]
-IDS = ["tiles-int4", "tiles-int8", "wide"]
+def blocks(qlen, G, rows):
+    """(t_first, t_last) of each row block of `rows` (token, head) rows over a qlen-token chunk with G heads."""
+    for r0 in range(0, qlen * G, rows):
+        yield r0 // G, (min(qlen * G, r0 + rows) - 1) // G
 
 
-def out_of_row(lead, int4, wide=False):
+# the tile kernel's 192-row blocks at GQA 1, 6 and 8, the wide kernel's 128-row blocks at GQA 16
+KERNELS = [dict(int4=True, G=6, rows=192), dict(int4=True, G=8, rows=192), dict(int4=True, G=1, rows=192),
+           dict(int4=False, G=6, rows=192), dict(int4=True, wide=True, G=16, rows=128)]
+IDS = ["tiles-int4-g6", "tiles-int4-g8", "tiles-int4-g1", "tiles-int8-g6", "wide-g16"]
+
+
+def out_of_row(lead, int4, G, rows, wide=False):
     bad = []
     for n, qlen, splits in shapes():
-        bq = 32
-        for t0 in range(0, qlen, bq):
+        for t_first, t_last in blocks(qlen, G, rows):
             for split in range(splits):
-                reads, _ = walk(n, qlen, t0, bq, split, splits, int4, lead, wide)
+                reads, _ = walk(n, qlen, t_first, t_last, split, splits, int4, lead, wide)
                 row = -(-n // 16)
-                bad += [(n, qlen, splits, t0, split, t, i) for t, i in reads if i >= row]
+                bad += [(n, qlen, splits, t_first, split, t, i) for t, i in reads if i >= row]
     return bad
 
 
@@ -134,10 +142,11 @@ def test_every_table_read_stays_in_the_row(kernel):
 def test_each_tile_reads_its_own_blocks(kernel):
     lead = steady_lead()
     for n, qlen, splits in shapes():
-        for t0 in range(0, qlen, 32):
+        for t_first, t_last in blocks(qlen, kernel["G"], kernel["rows"]):
             for split in range(splits):
-                reads, expected = walk(n, qlen, t0, 32, split, splits, kernel["int4"], lead, kernel.get("wide", False))
-                assert reads == expected, (n, qlen, splits, t0, split)
+                reads, expected = walk(n, qlen, t_first, t_last, split, splits, kernel["int4"], lead,
+                                       kernel.get("wide", False))
+                assert reads == expected, (n, qlen, splits, t_first, split)
 
 
 @pytest.mark.parametrize("kernel", KERNELS, ids=IDS)

@@ -26,7 +26,7 @@ struct PrefillParams {
   float *so;  // split partials: [token, head, split, HS] fp32, stats [token, head, split]
   float *smax, *ssum;
   int64_t sos0, sos1, sts0, sts1;
-  int32_t num_seqs, num_q_heads, num_kv_heads, block_size, num_splits, bq;
+  int32_t num_seqs, num_q_heads, num_kv_heads, block_size, num_splits;
   uint32_t bs_magic, bs_shift;
   float scale_log2;
   const float *qsigns;     // forward rotation of the query rows as they load (null: q in the cache's domain)
@@ -210,8 +210,8 @@ __device__ __forceinline__ u32x2_t i8_quad_bf16(uint32_t x) {
                  pack_bf16x2((float)((u >> 16) & 0xFFu), (float)(u >> 24))};
 }
 
-// The prefill on 32x32x16 MFMAs (qp_prefill_wide.hip), head 128 or 256, or 512 with int4 keys (at least 2 key
-// splits): grid (row blocks of prefill_wide_rows(head size) (token, query head) pairs, KV heads, key splits).
+// The prefill on 32x32x16 MFMAs (qp_prefill_wide.hip), head 128, or 512 with int4 keys (at least 2 key splits): grid
+// (row blocks of prefill_wide_rows(head size) (token, query head) pairs, KV heads, key splits).
 int prefill_wide_rows(int head_size);
 void prefill_wide(const PrefillParams &p, int head_size, int key_format, dim3 grid, bool span, hipStream_t s);
 

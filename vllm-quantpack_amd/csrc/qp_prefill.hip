@@ -8,9 +8,10 @@
 // s_k scale for int8 keys (both operands exact bf16 integers), P_v16 = bf16(P s_v) feeding both the PV product
 // and the zero-point sum (int4_kv.py:90-94), l from the unrounded P, causal within each sequence's query chunk.
 //
-// MI355X design. A workgroup of 4 waves (one per SIMD) owns (query block, KV head, key split). The query block holds
-// BQ tokens x the G query heads of the KV head, cut into 4 * NT row tiles of 16 rows; wave w owns tiles w, w + 4,
-// w + 8, so each K / V operand read from LDS feeds NT MFMAs and every K/V tile is dequantised once for all G heads.
+// MI355X design. A workgroup of 4 waves (one per SIMD) owns (row block, KV head, key split). A row block is 64 NT
+// consecutive (token, query head) pairs of one sequence in token-major order, so any GQA width fills it, cut into
+// 4 * NT row tiles of 16 rows; wave w owns tiles w, w + 4, w + 8, so each K / V operand read from LDS feeds NT MFMAs
+// and every K/V tile is dequantised once for all the block's rows.
 // Per 32-key tile, with one barrier:
 //   * the tile's two 16-key page runs come HBM -> LDS (global_load_lds_dwordx4) into one of three packed slots,
 //     issued four tiles ahead of the tile whose PV runs, from one scalar base per page run and fixed lane offsets;
@@ -36,6 +37,9 @@
 #include <type_traits>
 
 namespace qp {
+
+// row_pos of a row past the block's last (token, head) pair: below every key, as a row without keys, but not stored
+constexpr int kPfNoRow = -0x7FFFFFFF - 1;
 
 // K part of the unpack: bf16 K rows kd[key][channel], 8 channels per dword of int4 codes (4 of int8).
 template <int HS, int KFMT>
@@ -121,7 +125,7 @@ struct PfRows {
   bf16x8_t qop[NT][HS / 32];
   f32x4_t acc[NT][17];  // O^T tiles: tile b row j -> channel 16 b + 4 g + j; tile HS/16 row 0 = zp sum (17 = 256 / 16 + 1)
   float qsum[NT], m[NT], l[NT];
-  int row_pos[NT];
+  int row_pos[NT];  // the row's position in its sequence (< 0: a context shorter than the chunk), or kPfNoRow
 };
 
 // The unpack of one tile cut into stages that pf_iter spreads over its MFMA steps (each stage is a few LDS operations
@@ -487,25 +491,26 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
   const int col = lane & 15, g = lane >> 4;
   const int h = blockIdx.y;
   const int split = blockIdx.z;
-  const int BQ = p.bq;
-  // query block -> sequence: sequence s owns blocks [cu_q[s] / BQ + s, cu_q[s + 1] / BQ + s + 1)
+  const int G = p.num_q_heads / p.num_kv_heads;
+  constexpr int kRows = kPfWaves * NT * 16;  // (token, query head) rows per workgroup
+  // row block -> sequence: sequence s's rows (cu_q[s] G .. cu_q[s + 1] G) own blocks [cu_q[s] G / kRows + s, ...)
   const int blk = blockIdx.x;
   int lo = 0, hi = p.num_seqs - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
-    if (p.cu_q[mid] / BQ + mid <= blk) lo = mid;
+    if ((int)(((int64_t)p.cu_q[mid] * G) / kRows) + mid <= blk) lo = mid;
     else hi = mid - 1;
   }
   const int seq = lo;
   const int q0 = p.cu_q[seq], qlen = p.cu_q[seq + 1] - q0;
-  const int t0 = (blk - (q0 / BQ + seq)) * BQ;  // first local token of this block
-  if (t0 < 0 || t0 >= qlen) return;
+  const int nrows = qlen * G;
+  const int r0 = (blk - (int)(((int64_t)q0 * G) / kRows) - seq) * kRows;  // first local row of the block
+  if (r0 < 0 || r0 >= nrows) return;
   if (p.skip_seq && p.skip_seq[seq] >= 0) return;
   const int n = p.used_k[seq];
-  const int G = p.num_q_heads / p.num_kv_heads;
-  const int ntok = min(BQ, qlen - t0);
-  const int first_pos = n - qlen + t0;
-  const int kend = max(0, min(n, first_pos + ntok));  // keys any row of the block can see
+  const int t_first = r0 / G, t_last = (min(nrows, r0 + kRows) - 1) / G;
+  const int first_pos = n - qlen + t_first;
+  const int kend = max(0, min(n, n - qlen + t_last + 1));  // keys any row of the block can see
   // key split: the split-KV segment rule shared with qp_merge_segments
   const int S = p.num_splits;
   const int seg = (n + S * QP_DECODE_TILE - 1) / (S * QP_DECODE_TILE) * QP_DECODE_TILE;
@@ -513,16 +518,17 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
   const int ke = uniform(min(kend, kb + seg));
   if (S > 1 && kb >= n) return;  // inactive segment: the merge does not read it
 
-  // ---- the wave's row tiles: tile tt = w + 4 jt is (query head tt % G, tokens 16 (tt / G) .. + 15 of the block)
+  // ---- the wave's row tiles: tile tt = w + 4 jt holds rows r0 + 16 tt .. + 15 of the block, row r being (token
+  // r / G, query head r % G): any GQA width fills the tiles
   PfRows<HS, NT> r;
 #pragma unroll
   for (int jt = 0; jt < NT; ++jt) {
     const int tt = w + kPfWaves * jt;
-    const int jh = tt % G, sb = tt / G;
-    const int tok = t0 + 16 * sb + col;
-    const bool rv = 16 * sb < BQ && tok < qlen;
-    r.row_pos[jt] = rv ? first_pos + 16 * sb + col : -1;
-    const uint16_t *qr = p.q + (int64_t)(q0 + (rv ? tok : 0)) * p.qs0 + (int64_t)(h * G + (rv ? jh : 0)) * p.qs1;
+    const int rr = r0 + 16 * tt + col;
+    const bool rv = rr < nrows;
+    const int tok = rv ? rr / G : 0, jh = rv ? rr % G : 0;
+    r.row_pos[jt] = rv ? n - qlen + tok : kPfNoRow;
+    const uint16_t *qr = p.q + (int64_t)(q0 + tok) * p.qs0 + (int64_t)(h * G + jh) * p.qs1;
     uint32_t qw[HS / 8];  // channels (HS / 4) g .. + HS / 4 of the row, two per dword (rotated when asked)
     load_query_row<HS / 4>(qw, qr, rv, p.qsigns, g);
     float qs = 0.f;  // the row's query sum: the 128 offset of the key operands (and the int4 zero point) folds into it
@@ -722,10 +728,11 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
     l += shfl_xor_f(l, 16);
     l += shfl_xor_f(l, 32);
     const float csum = __shfl(r.acc[jt][HS / 16][0], col, 64);
-    const bool valid = r.row_pos[jt] >= 0;  // the same for the four lanes of a row (lanes col + 16 g)
-    const int tt = w + kPfWaves * jt;
-    const int64_t tok = q0 + t0 + 16 * (tt / G) + col;
-    const int64_t head = h * G + tt % G;
+    const bool valid = r.row_pos[jt] != kPfNoRow;  // the same for the four lanes of a row (lanes col + 16 g)
+    // the row's token from its position (live for the mask), its head without a division
+    const int tl = valid ? r.row_pos[jt] - (n - qlen) : 0;
+    const int64_t tok = q0 + tl;
+    const int64_t head = h * G + (valid ? r0 + 16 * (w + kPfWaves * jt) + col - tl * G : 0);
     if (S == 1) {
       const float inv = l > 0.f ? 1.f / l : 0.f;
       uint16_t *orow = p.out + tok * p.os0 + head * p.os1;
@@ -778,26 +785,37 @@ using namespace qp;
 
 namespace {
 
-// Row tiles per wave (NT) and query tokens per workgroup (BQ) for a GQA group of G heads: BQ / 16 = k token
-// sub-blocks with k G <= 12 row tiles, and no more than the longest query chunk needs.
-void prefill_geometry(int G, int max_query_len, int *nt, int *bq) {
-  int k = 12 / G;
-  const int need = (max_query_len + 15) / 16;
-  if (k > need) k = need < 1 ? 1 : need;
-  *nt = (k * G + kPfWaves - 1) / kPfWaves;
-  *bq = 16 * k;
+// Row tiles per wave: 3 (192 (token, query head) rows per workgroup), or fewer when the longest chunk holds fewer rows.
+int prefill_nt(int G, int max_query_len) {
+  const int64_t rows = (int64_t)(max_query_len > 0 ? max_query_len : 1) * G;
+  return rows > 128 ? 3 : rows > 64 ? 2 : 1;
 }
 
-// Key splits per query block: enough workgroups for one per CU, each split keeping >= 1024 keys.
-int prefill_splits(const qp_paged_cache *cache, const qp_prefill_args *a, int bq) {
+// Key splits for `wgs` workgroups (row blocks x KV heads) before splitting: the count, from min_s up to one split per
+// 1024 keys of the longest context (at most 64), whose workgroups take the least time, as rounds over the CUs times
+// a split's tiles plus about 8 tiles of fixed cost (the pipeline's fill, the partial's store); the smallest count
+// within 2 % of that wins, as fewer partials cost less to merge. 128 workgroups on 256 CUs over 131072 keys:
+// 2 splits; 344: 8; 172 over 32768 keys: 4.
+int balanced_splits(int64_t wgs, const qp_prefill_args *a, int min_s) {
+  const int64_t cus = device_cus();
+  int max_s = a->max_seqlen_k / 1024;
+  if (max_s > 64) max_s = 64;
+  if (max_s < min_s) max_s = min_s;
+  const int64_t tiles = (a->max_seqlen_k + kPfKeys - 1) / kPfKeys;
+  auto cost = [&](int S) { return (double)((wgs * S + cus - 1) / cus) * (double)((tiles + S - 1) / S + 8); };
+  double best = cost(min_s);
+  for (int S = min_s + 1; S <= max_s; ++S) best = cost(S) < best ? cost(S) : best;
+  for (int S = min_s; S <= max_s; ++S)
+    if (cost(S) <= best * 1.02) return S;
+  return min_s;
+}
+
+// Key splits per row block of the tile kernel.
+int prefill_splits(const qp_paged_cache *cache, const qp_prefill_args *a, int nt) {
   if (a->num_splits > 0) return a->num_splits;
-  const int64_t blocks = ((int64_t)a->num_tokens + bq - 1) / bq;
-  const int64_t wgs = blocks * cache->num_kv_heads;
-  int s = (int)(device_cus() / (wgs > 0 ? wgs : 1));
-  const int by_len = a->max_seqlen_k / 1024;
-  if (s > by_len) s = by_len;
-  if (s > 64) s = 64;
-  return s < 1 ? 1 : s;
+  const int64_t rows = (int64_t)kPfWaves * 16 * nt;
+  const int64_t blocks = ((int64_t)a->num_tokens * (a->num_q_heads / cache->num_kv_heads) + rows - 1) / rows;
+  return balanced_splits(blocks * cache->num_kv_heads, a, 1);
 }
 
 int64_t partial_bytes(const qp_paged_cache *cache, const qp_prefill_args *a, int splits) {
@@ -820,46 +838,33 @@ void dispatch_nt(const PrefillParams &p, int nt, dim3 grid, bool span, hipStream
   else launch_prefill<HS, KFMT, 3>(p, grid, span, s);
 }
 
-// Which kernel serves a prefill: the 16-row-tile kernel above up to 12 query heads per KV head; the wide kernel
-// (qp_prefill_wide.hip: 128 or 256 (token, head) rows per workgroup on 32x32x16 MFMAs, any GQA width) above that and
-// for head 512 with int4 keys; the query-slice path for head 512 with int8 keys, whose 776-byte cells do not fit the
-// wide kernel's LDS plan, and for head 64, whose 4 QK steps per tile leave the MFMA kernels' unpack nothing to hide
-// behind. (At head 256 the wide kernel holds one 32-row tile per wave, so each K / V operand it reads
-// from LDS serves 32 rows against the tile kernel's 48: 6.3 against 3.3 ms on the 1024-token chunk over 131072 keys
-// with 6 query heads per KV head.)
+// Which kernel serves a prefill (measured over 1024-token chunks at contexts of 32768 and 131072 keys):
+//   * head 256, and head 128 below 8 query heads per KV head: the 16-row-tile kernel above, whose 192-row blocks hold
+//     (token, head) pairs at any GQA width. At head 256 with 16 heads per KV head it takes 1.63 ms against the wide
+//     kernel's 1.72 (one 32-row tile per wave there: each K / V operand read from LDS serves 32 rows against 48);
+//   * head 128 from 8 query heads per KV head, and head 512 with int4 keys: the wide kernel (qp_prefill_wide.hip,
+//     32x32x16 MFMAs, 64 rows per wave at head 128): 1.77 against 1.97 ms at 8 heads per KV head, 0.94 against 1.29
+//     at 16;
+//   * head 512 with int8 keys, whose 776-byte cells do not fit the wide kernel's LDS plan, and head 64, whose 4 QK
+//     steps per tile leave the MFMA kernels' unpack nothing to hide behind: query slices of the split-KV kernel.
 enum class PrefillPath { kSlices, kTiles, kWide };
 
 PrefillPath prefill_path(const qp_paged_cache *cache, const qp_prefill_args *a) {
   const int hs = cache->head_size;
   if (hs == 512) return cache->key.format == QP_CODES_INT4 ? PrefillPath::kWide : PrefillPath::kSlices;
-  if (hs != 128 && hs != 256) return PrefillPath::kSlices;
-  return a->num_q_heads / cache->num_kv_heads > 12 ? PrefillPath::kWide : PrefillPath::kTiles;
+  if (hs == 128) return a->num_q_heads / cache->num_kv_heads >= 8 ? PrefillPath::kWide : PrefillPath::kTiles;
+  return hs == 256 ? PrefillPath::kTiles : PrefillPath::kSlices;
 }
 
-// Key splits of the wide kernel: the count whose workgroups (row blocks x KV heads x splits) fill the CUs in the
-// fewest rounds per unit of work, each split keeping >= 1024 keys (192 workgroups on 256 CUs: 4 splits, 3 full
-// rounds). At head 512 at least 2: that kernel writes split partials only, and the merge rotates and normalises.
+// Key splits of the wide kernel, as balanced_splits (192 workgroups on 256 CUs: 4 splits, 3 full rounds). At head 512
+// at least 2: that kernel writes split partials only, and the merge rotates and normalises.
 int wide_splits(const qp_paged_cache *cache, const qp_prefill_args *a) {
   const int min_s = cache->head_size == 512 ? 2 : 1;
   if (a->num_splits > 0) return a->num_splits > min_s ? a->num_splits : min_s;
   const int G = a->num_q_heads / cache->num_kv_heads;
   const int rows = prefill_wide_rows(cache->head_size);
   const int64_t blocks = ((int64_t)a->num_tokens * G + rows - 1) / rows;
-  const int64_t wgs = blocks * cache->num_kv_heads;
-  const int64_t cus = device_cus();
-  int max_s = a->max_seqlen_k / 1024;
-  if (max_s > 64) max_s = 64;
-  if (max_s < min_s) max_s = min_s;
-  int best = min_s;
-  double best_cost = (double)((wgs * min_s + cus - 1) / cus) / min_s;
-  for (int S = min_s + 1; S <= max_s; ++S) {
-    const double cost = (double)((wgs * S + cus - 1) / cus) / S;
-    if (cost < best_cost - 1e-9) {
-      best = S;
-      best_cost = cost;
-    }
-  }
-  return best;
+  return balanced_splits(blocks * cache->num_kv_heads, a, min_s);
 }
 
 }  // namespace
@@ -870,9 +875,8 @@ extern "C" int64_t qp_prefill_workspace_size(const qp_paged_cache *cache, const 
   const PrefillPath path = prefill_path(cache, a);
   if (path == PrefillPath::kSlices) return slice_prefill_workspace(cache, a);
   if (path == PrefillPath::kWide) return partial_bytes(cache, a, wide_splits(cache, a));
-  int nt, bq;
-  prefill_geometry(a->num_q_heads / cache->num_kv_heads, a->max_query_len, &nt, &bq);
-  return partial_bytes(cache, a, prefill_splits(cache, a, bq));
+  return partial_bytes(cache, a, prefill_splits(cache, a, prefill_nt(a->num_q_heads / cache->num_kv_heads,
+                                                                    a->max_query_len)));
 }
 
 namespace qp {
@@ -908,9 +912,8 @@ int prefill_run(const qp_paged_cache *cache, const qp_prefill_args *a, const int
   const PrefillPath path = prefill_path(cache, a);
   if (path == PrefillPath::kSlices) return slice_prefill(cache, a, skip_seq, s);
   const bool wide = path == PrefillPath::kWide;
-  int nt = 0, bq = 0;
-  if (!wide) prefill_geometry(G, a->max_query_len, &nt, &bq);
-  int splits = wide ? wide_splits(cache, a) : prefill_splits(cache, a, bq);
+  const int nt = wide ? 0 : prefill_nt(G, a->max_query_len);
+  int splits = wide ? wide_splits(cache, a) : prefill_splits(cache, a, nt);
   if (splits > 1 && (!a->workspace || a->workspace_bytes < partial_bytes(cache, a, splits))) {
     QP_REQUIRE(a->num_splits == 0, "qp_prefill: workspace too small for the requested splits");
     splits = 1;  // automatic choice without (enough) workspace: one workgroup per query block and KV head
@@ -959,17 +962,16 @@ int prefill_run(const qp_paged_cache *cache, const qp_prefill_args *a, const int
   p.num_kv_heads = cache->num_kv_heads;
   p.block_size = cache->block_size;
   p.num_splits = splits;
-  p.bq = bq;
   div_magic((uint32_t)cache->block_size, &p.bs_magic, &p.bs_shift);
   p.scale_log2 = a->softmax_scale * kLog2e;
   p.qsigns = a->query_signs;
   p.osigns = splits == 1 ? a->rht_signs : nullptr;  // split partials are rotated back by the merge
   p.out_scale = a->rht_out_scale;
   p.skip_seq = skip_seq;
-  // sequence s owns query blocks [cu_q[s] / BQ + s, cu_q[s + 1] / BQ + s + 1) (the wide kernel: row blocks
-  // [cu_q[s] G / 256 + s, cu_q[s + 1] G / 256 + s + 1)): an upper bound known on the host
-  const unsigned blocks = wide ? (unsigned)((int64_t)a->num_tokens * G / prefill_wide_rows(hs) + a->num_seqs)
-                               : (unsigned)(a->num_tokens / bq + a->num_seqs);
+  // sequence s owns row blocks [cu_q[s] G / R + s, cu_q[s + 1] G / R + s + 1) of R rows each: an upper bound known on
+  // the host
+  const int64_t rows_per_block = wide ? prefill_wide_rows(hs) : (int64_t)kPfWaves * 16 * nt;
+  const unsigned blocks = (unsigned)((int64_t)a->num_tokens * G / rows_per_block + a->num_seqs);
   const dim3 grid(blocks, cache->num_kv_heads, splits);
   const bool span = is_span_layout(cache) && cache->key.code_stride[0] < (int64_t(1) << 31);
   if (wide) {

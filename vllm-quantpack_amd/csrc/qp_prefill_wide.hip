@@ -6,10 +6,11 @@
 // or (q . (128 + k) - 128 sum(q)) s_k scale (int8 keys), P_v16 = bf16(P s_v) feeding both the PV product and the
 // zero-point sum (int4_kv.py:90-94), l from the unrounded P, causal within each sequence's query chunk.
 //
-// MI355X design. A workgroup of 4 waves (one per SIMD) owns 128 NT query rows of one KV head and one key split; the
-// rows are the chunk's (token, query head) pairs in token-major order, so any GQA group width packs them densely. Wave
-// w holds NT 32-row tiles (NT = 1 at head 256, where the query operands take 64 VGPRs per tile and the accumulators
-// 128 AGPRs; NT = 2 at head 128):
+// MI355X design (heads 128 and 512; head 256 runs on the 16-row-tile kernel, which serves it faster at every GQA
+// width). A workgroup of 4 waves (one per SIMD) owns 128 NT query rows of one KV head and one key split; the rows are
+// the chunk's (token, query head) pairs in token-major order, so any GQA group width packs them densely. Wave w holds
+// NT 32-row tiles (NT = 2 at head 128: 32 VGPRs of query operands and 64 AGPRs of accumulators per tile; NT = 1 at
+// head 512, below):
 //   * S^T = K Q^T on v_mfma_f32_32x32x16_bf16: the K tile (32 keys x 16 channels) is the A operand, read from LDS
 //     once per step and used by every row tile; the query rows are the B operand, held in VGPRs; these MFMAs are
 //     inline assembly writing VGPRs, so the compiler's own MFMAs (the PV below) keep AGPR accumulators;
@@ -821,15 +822,13 @@ void launch_wide(const PrefillParams &p, dim3 grid, bool span, hipStream_t s) {
 }
 
 int prefill_wide_rows(int head_size) {
-  return head_size >= 256 ? kPfWaves * 32 * wide_nt<256>() : kPfWaves * 32 * wide_nt<128>();
+  return head_size == 512 ? kPfWaves * 32 * wide_nt<512>() : kPfWaves * 32 * wide_nt<128>();
 }
 
+// Heads 128 and 512 (with int4 keys): the router's choices (head 256 runs on the tile kernel at every GQA width).
 void prefill_wide(const PrefillParams &p, int head_size, int key_format, dim3 grid, bool span, hipStream_t s) {
   if (head_size == 512) {
-    launch_wide<512, QP_CODES_INT4>(p, grid, span, s);  // int4 keys only (the router's choice)
-  } else if (head_size == 256) {
-    if (key_format == QP_CODES_INT4) launch_wide<256, QP_CODES_INT4>(p, grid, span, s);
-    else launch_wide<256, QP_CODES_INT8>(p, grid, span, s);
+    launch_wide<512, QP_CODES_INT4>(p, grid, span, s);
   } else {
     if (key_format == QP_CODES_INT4) launch_wide<128, QP_CODES_INT4>(p, grid, span, s);
     else launch_wide<128, QP_CODES_INT8>(p, grid, span, s);
