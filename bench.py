@@ -60,32 +60,36 @@ def decode_bench(torch, args):
                                 softmax_scale=w.softmax_scale, num_segments=S, softmax_segm_output=so,
                                 softmax_segm_max=sm, softmax_segm_expsum=ss) for d in copies]
     n = len(plans)
+    stream = torch.cuda.current_stream(dev)
+    # kernel durations: launches queued behind a spin that holds the stream, bracketed by one pair of events on that
+    # stream, so the average is the execution time in a full queue (an event pair around every launch would add its
+    # own dispatch overhead, about 3 us, to each): the split-KV decode kernel alone (the roofline's kernel) and the
+    # step's two launches (decode + merge). At least 200 launches each, whatever --steps is. They run before the timed
+    # steps, which therefore start on a GPU at its working clock, as in a serving loop (on an idle GPU the first
+    # timed steps measured about 3 us slower each).
+    reps = max(200, args.steps)
+
+    def queued(fn):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(SPIN_CYCLES)
+        a.record(stream)
+        for i in range(reps):
+            fn(plans[i % n])
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    kern_ms = queued(lambda pl: pl.decode())
+    pair_ms = queued(lambda pl: (pl.decode(), pl.merge()))
     for i in range(args.warmup):
         plans[i % n].run()
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
     # timed region: exactly `steps` decode steps (split-KV decode + merge), launched back to back
     t0 = time.perf_counter()
     for i in range(args.steps):
         plans[i % n].run()
     torch.cuda.synchronize()
     step_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    # kernel durations: `steps` launches queued behind a spin that holds the stream, bracketed by one pair of events
-    # on that stream, so the average is the execution time in a full queue (an event pair around every launch would
-    # add its own dispatch overhead, about 3 us, to each): the split-KV decode kernel alone (the roofline's kernel)
-    # and the step's two launches (decode + merge).
-    def queued(fn):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda._sleep(SPIN_CYCLES)
-        a.record(stream)
-        for i in range(args.steps):
-            fn(plans[i % n])
-        b.record(stream)
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / args.steps
-
-    kern_ms = queued(lambda pl: pl.decode())
-    pair_ms = queued(lambda pl: (pl.decode(), pl.merge()))
     nbytes = synth.cache_bytes(w)
     result = dict(tokens_per_step=T, step_ms=step_ms, decode_kernel_us=kern_ms * 1e3, bytes=nbytes, segments=S,
                   pair_us=pair_ms * 1e3, out=out, w=w, copies=copies)

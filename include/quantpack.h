@@ -134,8 +134,9 @@ int qp_merge_segments(const qp_merge_args *args, qp_stream_t stream);
  * When the query blocks alone cannot fill the device, the keys of each block are split over workgroups
  * (num_splits, 0 = chosen for the device) whose fp32 partials go to the caller's workspace and are merged as in
  * qp_merge_segments; without enough workspace an automatic choice falls back to one split.
- * More than 12 query heads per KV head run a wide variant whose 32-row MFMA tiles hold (token, head) pairs. Head 512
- * with int4 keys runs that variant too, always with at least 2 splits; with int8 keys, and head 64, it runs the
+ * Rows are (token, query head) pairs, so any GQA width fills the MFMA tiles. Head 128 from 8 query heads per KV head
+ * runs a wide variant on 32-row MFMA tiles; head 512 with int4 keys runs that variant too, always with at least 2
+ * splits; with int8 keys, and head 64, it runs the
  * split-KV decode kernel over causal query slices of at most 4 tokens and merges. These paths need the workspace
  * (qp_prefill_workspace_size bytes, 256-byte aligned).
  * With rht_signs the result is rotated back, out = (o H D) * rht_out_scale, as qp_merge_segments does.
@@ -169,6 +170,23 @@ int qp_prefill(const qp_paged_cache *cache, const qp_prefill_args *args, qp_stre
 
 /* Workspace bytes qp_prefill uses for these arguments on the current device (0 when it does not split). */
 int64_t qp_prefill_workspace_size(const qp_paged_cache *cache, const qp_prefill_args *args);
+
+/*
+ * The same chunked prefill with the arithmetic of the reference's single-kernel alternative (prefill_sequence_i8 and
+ * its _attn_i8 kernel, int4_prefill.py:95-200), int4 caches, heads 128 / 256 / 512: each query row is split in the
+ * kernel into two int8 parts in log2 units, q ~ q_scale (hi + lo / 254) (int4_prefill.py:181-189); QK^T runs as
+ * integer MFMAs on the raw key nibbles, S = ((hi . k) 254 + lo . k - q_sum zp_k) (q_scale / 254) s_k; the
+ * probabilities enter PV as P16 = fp16(p s_v) on fp16 MFMAs (fp32 accumulation; the reference's fp16 accumulation
+ * within a tile is not reproduced), the value operand being the nibble minus its zero point.
+ * Arguments as qp_prefill, except: softmax_scale is the query scale in log2 units (the softmax scale times log2 e,
+ * rounded once to fp32, as torch applies the reference's Python scalar to an fp32 tensor), and rht_signs /
+ * query_signs must be NULL (QP_ERR_UNSUPPORTED otherwise: the query and the output are in the cache's domain, as in
+ * the reference). Key splits take qp_prefill_i8_workspace_size bytes of workspace (16-byte aligned).
+ */
+int qp_prefill_i8(const qp_paged_cache *cache, const qp_prefill_args *args, qp_stream_t stream);
+
+/* Workspace bytes qp_prefill_i8 uses for these arguments on the current device (0 when it does not split). */
+int64_t qp_prefill_i8_workspace_size(const qp_paged_cache *cache, const qp_prefill_args *args);
 
 /*
  * One attention step of a batch over the paged cache, routed on the device with no host synchronisation:

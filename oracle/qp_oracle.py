@@ -424,6 +424,75 @@ def prefill_dequant_attend(q_rot, views: CacheViews, block_row, n: int, scale: f
     return out.numpy()
 
 
+# ------------------------------------------------------------------ single-kernel int8 prefill (a14, _attn_i8)
+
+Q_LO = 254  # weight of the high int8 part of the query (int4_prefill.py:173)
+
+
+def quantize_query_i8(q_rot_bits, softmax_scale: float):
+    """The query split of `prefill_sequence_i8` (int4_prefill.py:181-189), in fp32 as torch runs it:
+    q = f32(q_rot) * f32(softmax_scale * LOG2E) (torch rounds the Python scalar to the tensor's fp32 first);
+    q_scale = max(max|q| / 127, 1e-20) per (token, head); qn = q / q_scale; hi = round(qn) and
+    lo = clamp(round((qn - hi) * 254), -127, 127), rounding half to even (torch.round); q_sum = sum(hi) * 254 + sum(lo)
+    (exact: the fp32 sums of these integers stay below 2^24).
+    q_rot_bits: bf16 bits [T, NQ, hs]. Returns (hi int8, lo int8, q_scale fp32 [T, NQ], q_sum int64 [T, NQ])."""
+    q = bf16_bits_to_f32(q_rot_bits) * np.float32(softmax_scale * LOG2E)
+    qs = np.maximum(np.abs(q).max(axis=-1) / np.float32(127.0), np.float32(1e-20)).astype(np.float32)
+    qn = (q / qs[..., None]).astype(np.float32)
+    hi = np.rint(qn).astype(np.float32)
+    lo = np.clip(np.rint((qn - hi) * np.float32(Q_LO)), -127, 127).astype(np.float32)
+    q_sum = hi.astype(np.int64).sum(-1) * Q_LO + lo.astype(np.int64).sum(-1)
+    return hi.astype(np.int8), lo.astype(np.int8), qs, q_sum
+
+
+def i8_scores(hi, lo, q_sum, qs, kcodes, kwords) -> np.ndarray:
+    """The scores of `_attn_i8` (int4_prefill.py:136-138) of one query head over keys of one KV head, in log2 units:
+    S = ((hi . k) * 254 + lo . k - q_sum * zp_k), an exact int32 on the raw nibbles k (low nibble = even channel),
+    then fp32, times q_scale / 254 (fp32), times s_k. hi, lo: int8 [T, hs]; q_sum int [T]; qs fp32 [T];
+    kcodes uint8 [n, hs/2]; kwords uint32 [n]. Returns fp32 [T, n]."""
+    k = np.empty((kcodes.shape[0], 2 * kcodes.shape[1]), np.int64)
+    k[:, 0::2] = kcodes & 0xF
+    k[:, 1::2] = kcodes >> 4
+    zp, ks = int4_word_parts(kwords)
+    si = (hi.astype(np.int64) @ k.T) * Q_LO + lo.astype(np.int64) @ k.T - q_sum[:, None] * zp.astype(np.int64)[None, :]
+    qs_lo = (qs / np.float32(Q_LO)).astype(np.float32)
+    return (si.astype(np.float32) * qs_lo[:, None]).astype(np.float32) * ks[None, :]
+
+
+def prefill_i8_emulated(q_rot_bits, views: CacheViews, block_row, n: int, softmax_scale: float) -> np.ndarray:
+    """`_attn_i8` over one sequence (int4_prefill.py:95-172): the chunk's queries (the last T positions of a context of
+    n tokens, causal) against an int4 cache. Scores from i8_scores; softmax in base 2 against the row maximum; the
+    value operand nibble - zp (exact) and P16 = fp16(p * s_v) (:161-163); l the sum of the unrounded p; out = acc / l.
+    The reference adds each 64-key tile's fp16-accumulated PV into fp32 and rescales by its running maximum; here
+    everything after P16 is summed in fp64 against the final maximum (fp16 rounding is relative, so only values in
+    fp16's subnormal range depend on which maximum p is taken against). Returns fp64 [T, NQ, hs] (before the bf16
+    store)."""
+    hi, lo, qs, q_sum = quantize_query_i8(q_rot_bits, softmax_scale)
+    T, NQ, hs = hi.shape
+    kc, kw, vc, vw = gather(views, block_row, np.arange(n))
+    nkv = kc.shape[1]
+    g = NQ // nkv
+    pos = n - T + np.arange(T)
+    mask = np.arange(n)[None, :] > pos[:, None]
+    out = np.zeros((T, NQ, hs), np.float64)
+    for kvh in range(nkv):
+        v = np.empty((n, hs), np.float64)
+        v[:, 0::2] = vc[:, kvh] & 0xF
+        v[:, 1::2] = vc[:, kvh] >> 4
+        zp_v, s_v = int4_word_parts(vw[:, kvh])
+        v -= zp_v.astype(np.float64)[:, None]
+        for h in range(kvh * g, (kvh + 1) * g):
+            s = i8_scores(hi[:, h], lo[:, h], q_sum[:, h], qs[:, h], kc[:, kvh], kw[:, kvh]).astype(np.float64)
+            s = np.where(mask, -np.inf, s)
+            mx = s.max(axis=1, keepdims=True)
+            ok = np.isfinite(mx)
+            p = np.where(ok, np.exp2(s - np.where(ok, mx, 0.0)), 0.0)
+            p16 = (p.astype(np.float32) * s_v[None, :]).astype(np.float16).astype(np.float64)
+            l = p.sum(axis=1, keepdims=True)
+            out[:, h] = (p16 @ v) / np.where(l > 0, l, 1.0)
+    return out
+
+
 # ------------------------------------------------------------------------------------------- store (next-1)
 
 def round_half_away(x: np.ndarray) -> np.ndarray:

@@ -25,7 +25,8 @@ def _declared():
 
 def test_header_declares_the_entry_points():
     assert _declared() == sorted(["qp_unpack_segment", "qp_decode_splitkv", "qp_merge_segments", "qp_prefill",
-                                  "qp_prefill_workspace_size", "qp_attention", "qp_attention_workspace_size",
+                                  "qp_prefill_workspace_size", "qp_prefill_i8", "qp_prefill_i8_workspace_size",
+                                  "qp_attention", "qp_attention_workspace_size",
                                   "qp_attention_noalloc", "qp_store", "qp_rht", "qp_last_error", "qp_version"])
 
 

@@ -588,3 +588,103 @@ def test_store_takes_the_fused_multiply_add_code():
         zp = np.clip(O.round_half_away(-np.float32(lo) / scale), 0, 15).astype(np.float32)
         inv = np.float32(1.0) / scale
         assert O.round_half_away(np.float32(probe) * inv + zp) == muladd_code != fma_code
+
+
+# ----------------------------------------------------------------- single-kernel int8 prefill (a14, _attn_i8)
+
+def test_quantize_query_i8_known_answers():
+    """int4_prefill.py:181-189 by hand on a row whose scale is 1 (max |q| = 127 in log2 units): hi = round half to
+    even, lo = the rounded remainder in 1/254 units, q_sum = sum(hi) * 254 + sum(lo); a zero row takes the 1e-20 floor
+    and splits to zeros."""
+    scale = 1.0 / O.LOG2E                       # f32(scale * LOG2E) == 1.0
+    row = [127.0, 1.5, -2.25, 0.5, 3.75, -0.5, 0.0, -127.0]
+    q = np.array([row, [0.0] * 8], np.float32)[None]                      # [1 token, 2 heads, 8]
+    hi, lo, qs, q_sum = O.quantize_query_i8(O.f32_to_bf16_bits(q), scale)
+    assert qs[0, 0] == np.float32(1.0)
+    assert hi[0, 0].tolist() == [127, 2, -2, 0, 4, 0, 0, -127]
+    assert lo[0, 0].tolist() == [0, -127, -64, 127, -64, -127, 0, 0]    # -63.5 -> -64 (half to even)
+    assert q_sum[0, 0] == (127 + 2 - 2 + 4 - 127) * 254 + (-127 - 64 + 127 - 64 - 127)
+    assert qs[0, 1] == np.float32(1e-20) and not hi[0, 1].any() and not lo[0, 1].any() and q_sum[0, 1] == 0
+
+
+def test_quantize_query_i8_reconstructs_and_matches_torch():
+    """q ~ q_scale (hi + lo / 254) within half a 1/254 step (plus fp32 rounding); and torch running the reference's
+    own lines (int4_prefill.py:181-189) gives the same integers and scales bit for bit."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(21)
+    bits = O.f32_to_bf16_bits((rng.standard_normal((16, 6, 64)) * rng.lognormal(0, 1, (16, 6, 1))).astype(np.float32))
+    scale = 64 ** -0.5
+    hi, lo, qs, q_sum = O.quantize_query_i8(bits, scale)
+    q = O.bf16_bits_to_f32(bits).astype(np.float64) * np.float32(scale * O.LOG2E)
+    rec = qs[..., None].astype(np.float64) * (hi + lo / 254.0)
+    assert (np.abs(q - rec) <= qs[..., None] * (0.5 / 254 + 1e-5)).all()
+    tq = torch.from_numpy(O.bf16_bits_to_f32(bits)).float() * (scale * O.LOG2E)
+    t_scale = (tq.abs().amax(-1) / 127.0).clamp_min(1e-20)
+    tn = tq / t_scale[..., None]
+    t_hi = torch.round(tn)
+    t_lo = torch.round((tn - t_hi) * 254).clamp(-127, 127)
+    t_sum = (t_hi.sum(-1) * 254 + t_lo.sum(-1)).to(torch.int32)
+    assert (t_scale.numpy() == qs).all()
+    assert (t_hi.to(torch.int8).numpy() == hi).all() and (t_lo.to(torch.int8).numpy() == lo).all()
+    assert (t_sum.numpy() == q_sum).all()
+
+
+def test_i8_scores_brute_force():
+    """Integer dots and the two fp32 products of int4_prefill.py:136-138, term by term on a tiny case."""
+    rng = np.random.default_rng(22)
+    v, row = _tiny_cache(rng, 5, 1, 8, 16)
+    bits = O.f32_to_bf16_bits(rng.standard_normal((2, 1, 8)).astype(np.float32))
+    hi, lo, qs, q_sum = O.quantize_query_i8(bits, 0.3)
+    kc, kw, _, _ = O.gather(v, row, np.arange(5))
+    got = O.i8_scores(hi[:, 0], lo[:, 0], q_sum[:, 0], qs[:, 0], kc[:, 0], kw[:, 0])
+    for t in range(2):
+        for j in range(5):
+            codes = [(int(kc[j, 0, c // 2]) >> (4 * (c % 2))) & 0xF for c in range(8)]
+            w = int(kw[j, 0])
+            dot = sum((int(hi[t, 0, c]) * 254 + int(lo[t, 0, c])) * codes[c] for c in range(8)) - int(q_sum[t, 0]) * (w & 0xF)
+            ks = np.uint32(w & 0xFFFFFFF0).view(np.float32)
+            want = np.float32(np.float32(dot) * np.float32(qs[t, 0] / np.float32(254))) * ks
+            assert got[t, j] == want, (t, j)
+
+
+def _i8_case(seed=23, T=48, n=600, nq=6, nkv=2, hs=32):
+    rng = np.random.default_rng(seed)
+    v, row = _tiny_cache(rng, n, nkv, hs, 16)
+    q = O.round_bf16(rng.standard_normal((T, nq, hs)).astype(np.float32))
+    K, V = O.dequant_f64(v, row, n)
+    return v, row, q, O.attention_f64(q, K, V, n, hs ** -0.5)
+
+
+def test_prefill_i8_emulated_matches_fp64():
+    v, row, q, ref = _i8_case()
+    got = O.prefill_i8_emulated(O.f32_to_bf16_bits(q), v, row, 600, 32 ** -0.5)
+    assert O.relerr(got, ref) < 2e-3 and O.max_row_relerr(got, ref) < 5e-3
+
+
+@pytest.mark.parametrize("kind", ["hi-only", "no-key-zero-point", "no-value-zero-point", "q-sum-weight-256"])
+def test_prefill_i8_planted_mistakes_fail_the_fp64_check(monkeypatch, kind):
+    """Each variant departs from int4_prefill.py:136-165 in one term and must fail the check the real one passes.
+    hi-only is the one-int8 split whose error the reference's docstring puts at about 1.3e-2 (:104-105)."""
+    v, row, q, ref = _i8_case(seed=24)
+    bits = O.f32_to_bf16_bits(q)
+    good = O.relerr(O.prefill_i8_emulated(bits, v, row, 600, 32 ** -0.5), ref)
+    real_q, real_parts, real_scores = O.quantize_query_i8, O.int4_word_parts, O.i8_scores
+    if kind == "hi-only":
+        monkeypatch.setattr(O, "quantize_query_i8", lambda b, s: (lambda h, l, qs, sm: (
+            h, np.zeros_like(l), qs, h.astype(np.int64).sum(-1) * O.Q_LO))(*real_q(b, s)))
+    elif kind == "no-key-zero-point":
+        monkeypatch.setattr(O, "i8_scores", lambda hi, lo, sm, qs, kc, kw: real_scores(
+            hi, lo, np.zeros_like(sm), qs, kc, kw))
+    elif kind == "no-value-zero-point":
+        calls = {"n": 0}
+
+        def parts(w):
+            calls["n"] += 1
+            zp, sc = real_parts(w)
+            return (np.zeros_like(zp) if calls["n"] % 2 == 1 else zp), sc   # the value half's call comes first
+        monkeypatch.setattr(O, "int4_word_parts", parts)
+    elif kind == "q-sum-weight-256":  # the zero-point term's query sum with the hi part weighted 256, not 254
+        monkeypatch.setattr(O, "quantize_query_i8", lambda b, s: (lambda h, l, qs, sm: (
+            h, l, qs, h.astype(np.int64).sum(-1) * 256 + l.astype(np.int64).sum(-1)))(*real_q(b, s)))
+    bad = O.relerr(O.prefill_i8_emulated(bits, v, row, 600, 32 ** -0.5), ref)
+    assert good < 2e-3 and bad > 4 * good, (good, bad)

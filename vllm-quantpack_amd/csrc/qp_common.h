@@ -336,11 +336,13 @@ __device__ __forceinline__ void dma16_saddr(const uint8_t *base, uint32_t voff, 
   const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)base);
   const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)((uintptr_t)base >> 32));
   const uint64_t b = ((uint64_t)hi << 32) | (uint64_t)lo;
+  // the LDS address too (a caller's sum of uniform values may sit in a VGPR inside a lane-masked branch)
+  const uint32_t l = (uint32_t)__builtin_amdgcn_readfirstlane(lds);
   if constexpr (NT)
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(b), "s"(lds)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(b), "s"(l)
                  : "memory", "m0");
   else
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(b), "s"(lds)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(b), "s"(l)
                  : "memory", "m0");
 #endif
 }

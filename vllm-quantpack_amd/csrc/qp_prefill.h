@@ -210,6 +210,15 @@ __device__ __forceinline__ u32x2_t i8_quad_bf16(uint32_t x) {
                  pack_bf16x2((float)((u >> 16) & 0xFFu), (float)(u >> 24))};
 }
 
+// Host helpers shared by the prefill entry points (qp_prefill.hip).
+// Key splits for `wgs` workgroups (row blocks x KV heads): the count from min_s up that takes the least time on this
+// device's CUs.
+int balanced_splits(int64_t wgs, const qp_prefill_args *a, int min_s);
+// Kernel parameters of a prefill over `cache` with `splits` key splits (partials in a->workspace when splits > 1).
+PrefillParams prefill_params(const qp_paged_cache *cache, const qp_prefill_args *a, int splits);
+// The log-sum-exp merge of a split prefill's partials into a->out (inverse rotation when a->rht_signs is set).
+int prefill_merge(const PrefillParams &p, const qp_prefill_args *a, int hs, const int32_t *skip_seq, hipStream_t s);
+
 // The prefill on 32x32x16 MFMAs (qp_prefill_wide.hip), head 128, or 512 with int4 keys (at least 2 key splits): grid
 // (row blocks of prefill_wide_rows(head size) (token, query head) pairs, KV heads, key splits).
 int prefill_wide_rows(int head_size);

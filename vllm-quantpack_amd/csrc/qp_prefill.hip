@@ -781,15 +781,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
 
 }  // namespace qp
 
-using namespace qp;
-
-namespace {
-
-// Row tiles per wave: 3 (192 (token, query head) rows per workgroup), or fewer when the longest chunk holds fewer rows.
-int prefill_nt(int G, int max_query_len) {
-  const int64_t rows = (int64_t)(max_query_len > 0 ? max_query_len : 1) * G;
-  return rows > 128 ? 3 : rows > 64 ? 2 : 1;
-}
+namespace qp {
 
 // Key splits for `wgs` workgroups (row blocks x KV heads) before splitting: the count, from min_s up to one split per
 // 1024 keys of the longest context (at most 64), whose workgroups take the least time, as rounds over the CUs times
@@ -808,6 +800,18 @@ int balanced_splits(int64_t wgs, const qp_prefill_args *a, int min_s) {
   for (int S = min_s; S <= max_s; ++S)
     if (cost(S) <= best * 1.02) return S;
   return min_s;
+}
+
+}  // namespace qp
+
+using namespace qp;
+
+namespace {
+
+// Row tiles per wave: 3 (192 (token, query head) rows per workgroup), or fewer when the longest chunk holds fewer rows.
+int prefill_nt(int G, int max_query_len) {
+  const int64_t rows = (int64_t)(max_query_len > 0 ? max_query_len : 1) * G;
+  return rows > 128 ? 3 : rows > 64 ? 2 : 1;
 }
 
 // Key splits per row block of the tile kernel.
@@ -881,47 +885,10 @@ extern "C" int64_t qp_prefill_workspace_size(const qp_paged_cache *cache, const 
 
 namespace qp {
 
-int prefill_run(const qp_paged_cache *cache, const qp_prefill_args *a, const int32_t *skip_seq, hipStream_t s) {
-  QP_REQUIRE(cache && a, "qp_prefill: null argument");
-  QP_REQUIRE(cache->key.codes && cache->key.words && cache->value.codes && cache->value.words,
-             "qp_prefill: null cache view");
-  QP_REQUIRE(a->query && a->cu_seqlens_q && a->seqused_k && a->block_table && a->out, "qp_prefill: null tensor");
+// Kernel parameters of a prefill over `cache` with `splits` key splits (partials in a->workspace when splits > 1):
+// strides, the row-block split, the query scale in log2 units and the fused rotations.
+PrefillParams prefill_params(const qp_paged_cache *cache, const qp_prefill_args *a, int splits) {
   const int hs = cache->head_size;
-  QP_SUPPORTED(hs == 64 || hs == 128 || hs == 256 || hs == 512, "qp_prefill: head size must be 64, 128, 256 or 512");
-  QP_REQUIRE(cache->key.format == QP_CODES_INT4 || cache->key.format == QP_CODES_INT8, "qp_prefill: bad key format");
-  QP_REQUIRE(cache->value.format == QP_CODES_INT4, "qp_prefill: values must be int4");
-  QP_REQUIRE(cache->num_kv_heads > 0 && a->num_q_heads > 0 && a->num_q_heads % cache->num_kv_heads == 0,
-             "qp_prefill: query heads must be a multiple of KV heads");
-  const int G = a->num_q_heads / cache->num_kv_heads;
-  QP_SUPPORTED(cache->block_size >= 16 && cache->block_size % 16 == 0,
-               "qp_prefill: block size must be a multiple of 16");
-  QP_REQUIRE(a->num_seqs >= 0 && a->num_tokens >= 0 && a->max_query_len >= 0 && a->max_seqlen_k >= 0,
-             "qp_prefill: bad sizes");
-  QP_REQUIRE(a->num_splits >= 0 && a->num_splits <= 2048, "qp_prefill: 0..2048 splits");
-  for (int i = 0; i < 3; ++i)
-    QP_REQUIRE(cache->key.code_stride[i] % 4 == 0 && cache->value.code_stride[i] % 4 == 0,
-               "qp_prefill: code strides must be multiples of 4 bytes");
-  QP_REQUIRE(aligned(cache->key.codes, 4) && aligned(cache->value.codes, 4) && aligned(cache->key.words, 4) &&
-                 aligned(cache->value.words, 4),
-             "qp_prefill: cache views must be 4-byte aligned");
-  QP_REQUIRE(aligned(a->query, 16) && a->query_stride[0] % 8 == 0 && a->query_stride[1] % 8 == 0,
-             "qp_prefill: query rows must be 16-byte aligned");
-  QP_REQUIRE(aligned(a->out, 8) && a->out_stride[0] % 4 == 0 && a->out_stride[1] % 4 == 0,
-             "qp_prefill: output rows must be 8-byte aligned");
-  if (a->num_seqs == 0 || a->num_tokens == 0) return QP_OK;
-  const PrefillPath path = prefill_path(cache, a);
-  if (path == PrefillPath::kSlices) return slice_prefill(cache, a, skip_seq, s);
-  const bool wide = path == PrefillPath::kWide;
-  const int nt = wide ? 0 : prefill_nt(G, a->max_query_len);
-  int splits = wide ? wide_splits(cache, a) : prefill_splits(cache, a, nt);
-  if (splits > 1 && (!a->workspace || a->workspace_bytes < partial_bytes(cache, a, splits))) {
-    QP_REQUIRE(a->num_splits == 0, "qp_prefill: workspace too small for the requested splits");
-    splits = 1;  // automatic choice without (enough) workspace: one workgroup per query block and KV head
-  }
-  QP_REQUIRE(!wide || hs != 512 || splits > 1,
-             "qp_prefill: head 512 needs a workspace of qp_prefill_workspace_size bytes (split partials)");
-  QP_REQUIRE(splits == 1 || aligned(a->workspace, 16), "qp_prefill: workspace must be 16-byte aligned");
-
   PrefillParams p;
   p.kcodes = static_cast<const uint8_t *>(cache->key.codes);
   p.ks0 = cache->key.code_stride[0];
@@ -967,6 +934,80 @@ int prefill_run(const qp_paged_cache *cache, const qp_prefill_args *a, const int
   p.qsigns = a->query_signs;
   p.osigns = splits == 1 ? a->rht_signs : nullptr;  // split partials are rotated back by the merge
   p.out_scale = a->rht_out_scale;
+  p.skip_seq = nullptr;
+  return p;
+}
+
+// The log-sum-exp merge of a split prefill's partials (p.so / p.smax / p.ssum) into a->out, with the inverse
+// rotation when a->rht_signs is set.
+int prefill_merge(const PrefillParams &p, const qp_prefill_args *a, int hs, const int32_t *skip_seq,
+                  hipStream_t s) {
+  qp_merge_args m = {};
+  m.segm_output = p.so;
+  m.segm_output_stride[0] = p.sos0;
+  m.segm_output_stride[1] = p.sos1;
+  m.segm_output_stride[2] = hs;
+  m.segm_max = p.smax;
+  m.segm_expsum = p.ssum;
+  m.segm_stat_stride[0] = p.sts0;
+  m.segm_stat_stride[1] = p.sts1;
+  m.cu_seqlens_q = a->cu_seqlens_q;
+  m.seqused_k = a->seqused_k;
+  m.num_seqs = a->num_seqs;
+  m.num_tokens = a->num_tokens;
+  m.num_q_heads = a->num_q_heads;
+  m.head_size = hs;
+  m.num_segments = p.num_splits;
+  m.out = a->out;
+  m.out_stride[0] = a->out_stride[0];
+  m.out_stride[1] = a->out_stride[1];
+  m.rht_signs = a->rht_signs;
+  m.rht_out_scale = a->rht_out_scale;
+  return merge_routed(&m, nullptr, nullptr, 0, skip_seq, s);
+}
+
+int prefill_run(const qp_paged_cache *cache, const qp_prefill_args *a, const int32_t *skip_seq, hipStream_t s) {
+  QP_REQUIRE(cache && a, "qp_prefill: null argument");
+  QP_REQUIRE(cache->key.codes && cache->key.words && cache->value.codes && cache->value.words,
+             "qp_prefill: null cache view");
+  QP_REQUIRE(a->query && a->cu_seqlens_q && a->seqused_k && a->block_table && a->out, "qp_prefill: null tensor");
+  const int hs = cache->head_size;
+  QP_SUPPORTED(hs == 64 || hs == 128 || hs == 256 || hs == 512, "qp_prefill: head size must be 64, 128, 256 or 512");
+  QP_REQUIRE(cache->key.format == QP_CODES_INT4 || cache->key.format == QP_CODES_INT8, "qp_prefill: bad key format");
+  QP_REQUIRE(cache->value.format == QP_CODES_INT4, "qp_prefill: values must be int4");
+  QP_REQUIRE(cache->num_kv_heads > 0 && a->num_q_heads > 0 && a->num_q_heads % cache->num_kv_heads == 0,
+             "qp_prefill: query heads must be a multiple of KV heads");
+  const int G = a->num_q_heads / cache->num_kv_heads;
+  QP_SUPPORTED(cache->block_size >= 16 && cache->block_size % 16 == 0,
+               "qp_prefill: block size must be a multiple of 16");
+  QP_REQUIRE(a->num_seqs >= 0 && a->num_tokens >= 0 && a->max_query_len >= 0 && a->max_seqlen_k >= 0,
+             "qp_prefill: bad sizes");
+  QP_REQUIRE(a->num_splits >= 0 && a->num_splits <= 2048, "qp_prefill: 0..2048 splits");
+  for (int i = 0; i < 3; ++i)
+    QP_REQUIRE(cache->key.code_stride[i] % 4 == 0 && cache->value.code_stride[i] % 4 == 0,
+               "qp_prefill: code strides must be multiples of 4 bytes");
+  QP_REQUIRE(aligned(cache->key.codes, 4) && aligned(cache->value.codes, 4) && aligned(cache->key.words, 4) &&
+                 aligned(cache->value.words, 4),
+             "qp_prefill: cache views must be 4-byte aligned");
+  QP_REQUIRE(aligned(a->query, 16) && a->query_stride[0] % 8 == 0 && a->query_stride[1] % 8 == 0,
+             "qp_prefill: query rows must be 16-byte aligned");
+  QP_REQUIRE(aligned(a->out, 8) && a->out_stride[0] % 4 == 0 && a->out_stride[1] % 4 == 0,
+             "qp_prefill: output rows must be 8-byte aligned");
+  if (a->num_seqs == 0 || a->num_tokens == 0) return QP_OK;
+  const PrefillPath path = prefill_path(cache, a);
+  if (path == PrefillPath::kSlices) return slice_prefill(cache, a, skip_seq, s);
+  const bool wide = path == PrefillPath::kWide;
+  const int nt = wide ? 0 : prefill_nt(G, a->max_query_len);
+  int splits = wide ? wide_splits(cache, a) : prefill_splits(cache, a, nt);
+  if (splits > 1 && (!a->workspace || a->workspace_bytes < partial_bytes(cache, a, splits))) {
+    QP_REQUIRE(a->num_splits == 0, "qp_prefill: workspace too small for the requested splits");
+    splits = 1;  // automatic choice without (enough) workspace: one workgroup per query block and KV head
+  }
+  QP_REQUIRE(!wide || hs != 512 || splits > 1,
+             "qp_prefill: head 512 needs a workspace of qp_prefill_workspace_size bytes (split partials)");
+  QP_REQUIRE(splits == 1 || aligned(a->workspace, 16), "qp_prefill: workspace must be 16-byte aligned");
+
+  PrefillParams p = prefill_params(cache, a, splits);
   p.skip_seq = skip_seq;
   // sequence s owns row blocks [cu_q[s] G / R + s, cu_q[s + 1] G / R + s + 1) of R rows each: an upper bound known on
   // the host
@@ -985,30 +1026,7 @@ int prefill_run(const qp_paged_cache *cache, const qp_prefill_args *a, const int
   }
   const int st = launch_status();
   if (st != QP_OK) return st;
-  if (splits > 1) {
-    qp_merge_args m = {};
-    m.segm_output = p.so;
-    m.segm_output_stride[0] = p.sos0;
-    m.segm_output_stride[1] = p.sos1;
-    m.segm_output_stride[2] = hs;
-    m.segm_max = p.smax;
-    m.segm_expsum = p.ssum;
-    m.segm_stat_stride[0] = p.sts0;
-    m.segm_stat_stride[1] = p.sts1;
-    m.cu_seqlens_q = a->cu_seqlens_q;
-    m.seqused_k = a->seqused_k;
-    m.num_seqs = a->num_seqs;
-    m.num_tokens = a->num_tokens;
-    m.num_q_heads = a->num_q_heads;
-    m.head_size = hs;
-    m.num_segments = splits;
-    m.out = a->out;
-    m.out_stride[0] = a->out_stride[0];
-    m.out_stride[1] = a->out_stride[1];
-    m.rht_signs = a->rht_signs;
-    m.rht_out_scale = a->rht_out_scale;
-    return merge_routed(&m, nullptr, nullptr, 0, skip_seq, s);
-  }
+  if (splits > 1) return prefill_merge(p, a, hs, skip_seq, s);
   return QP_OK;
 }
 

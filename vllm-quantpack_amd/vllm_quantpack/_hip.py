@@ -131,6 +131,8 @@ SIGNATURES = {
     "qp_merge_segments": (c_int32, [POINTER(MergeArgs), c_void_p]),
     "qp_prefill": (c_int32, [POINTER(PagedCache), POINTER(PrefillArgs), c_void_p]),
     "qp_prefill_workspace_size": (c_int64, [POINTER(PagedCache), POINTER(PrefillArgs)]),
+    "qp_prefill_i8": (c_int32, [POINTER(PagedCache), POINTER(PrefillArgs), c_void_p]),
+    "qp_prefill_i8_workspace_size": (c_int64, [POINTER(PagedCache), POINTER(PrefillArgs)]),
     "qp_attention": (c_int32, [POINTER(PagedCache), POINTER(AttentionArgs), c_void_p]),
     "qp_attention_workspace_size": (c_int64, [POINTER(PagedCache), POINTER(AttentionArgs)]),
     "qp_attention_noalloc": (c_int32, [POINTER(PagedCache), POINTER(AttentionArgs), c_void_p]),

@@ -5,13 +5,18 @@ attends with FlashAttention 2 and folds the segments by log-sum-exp (int4_prefil
 kernel (`qp_prefill`) reads the packed cache directly: it dequantises K/V tiles to exact bf16 integers in LDS and runs
 QK^T and PV on bf16 MFMA with an online softmax, so there is no scratch, no segment loop and no host synchronisation.
 `unpack_segment` remains, bit-exact with the reference's `_unpack_segment` / `_unpack_segment_i8`, for callers that
-want bf16 K/V.
+want bf16 K/V. `prefill_sequence_i8` keeps the reference's single-kernel alternative and its arithmetic (an int8
+split of the query, integer QK^T on the raw nibbles, fp16 PV: int4_prefill.py:95-200) on its own HIP kernel
+(`qp_prefill_i8`).
 """
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from .. import _hip
+
+LOG2E = 1.4426950408889634
 
 MAX_HEAD = 512       # largest head size of the MFMA prefill kernels (head 512: the wide kernel with int4 keys)
 SEGMENT = 16384      # the reference's unpack segment; kept for callers that size bf16 scratch the same way
@@ -57,10 +62,27 @@ def prefill_attention(q, k_cache, v_cache, k_scale_cache, v_scale_cache, out, *,
     When the chunk alone cannot fill the GPU, the keys are split over workgroups
     (num_splits, 0 = automatic) and merged; the fp32 partials go to a workspace from torch's caching allocator.
     max_seqlen_k bounds the automatic split count; without it the block table's capacity stands in (no host sync).
-    More than 12 query heads per KV head, and head 512 with int4 keys, run the library's wide kernel (rows as
-    (token, head) pairs on 32x32x16 MFMAs; at head 512 always key-split, so it takes a workspace); head 512 with int8
+    Rows are (token, query head) pairs, so any GQA width fills the kernels' tiles. Head 128 from 8 query heads per KV
+    head, and head 512 with int4 keys, run the library's wide kernel (32x32x16 MFMAs; at head 512 always key-split, so
+    it takes a workspace); head 512 with int8
     keys runs the split-KV decode kernel over causal query slices of the chunk and merges (the library picks the
     path)."""
+    cache, args = _prefill_args(q, k_cache, v_cache, k_scale_cache, v_scale_cache, out, cu_seqlens_q, seqused_k,
+                                block_table, max_seqlen_q, softmax_scale, max_seqlen_k, num_splits)
+    args.rht_signs = _hip.ptr(rht_signs)
+    args.rht_out_scale = float(rht_out_scale)
+    args.query_signs = _hip.ptr(query_signs)
+    lib = _hip.lib()
+    need = lib.qp_prefill_workspace_size(cache, args)
+    ws = torch.empty(need, dtype=torch.uint8, device=q.device) if need > 0 else None
+    args.workspace = _hip.ptr(ws)
+    args.workspace_bytes = need
+    _hip.check(lib.qp_prefill(cache, args, _hip.stream_of(q)), "prefill")
+
+
+def _prefill_args(q, k_cache, v_cache, k_scale_cache, v_scale_cache, out, cu_seqlens_q, seqused_k, block_table,
+                  max_seqlen_q, softmax_scale, max_seqlen_k, num_splits):
+    """(qp_paged_cache, qp_prefill_args) of a prefill call, without workspace or rotations."""
     hs = q.shape[2]
     cache = _hip.paged_cache(k_cache, v_cache, k_scale_cache, v_scale_cache, hs)
     if max_seqlen_k is None:
@@ -81,15 +103,26 @@ def prefill_attention(q, k_cache, v_cache, k_scale_cache, v_scale_cache, out, *,
     args.softmax_scale = float(softmax_scale)
     args.out = out.data_ptr()
     args.out_stride = _hip.I64x2(out.stride(0), out.stride(1))
-    args.rht_signs = _hip.ptr(rht_signs)
-    args.rht_out_scale = float(rht_out_scale)
-    args.query_signs = _hip.ptr(query_signs)
+    args.rht_out_scale = 1.0
+    return cache, args
+
+
+def prefill_attention_i8(q, k_cache, v_cache, k_scale_cache, v_scale_cache, out, *, cu_seqlens_q, seqused_k,
+                         block_table, max_seqlen_q, softmax_scale, max_seqlen_k=None, num_splits=0) -> None:
+    """prefill_attention with the arithmetic of the reference's single-kernel alternative (`_attn_i8`,
+    int4_prefill.py:95-172), on int4 caches with q and out in the cache's domain: each query row is split into two
+    int8 parts in log2 units (q_scale (hi + lo / 254), the split of int4_prefill.py:181-189, done in the kernel), QK^T
+    runs on int8 MFMAs over the raw key nibbles and PV on fp16 MFMAs with P16 = fp16(p s_v)."""
+    cache, args = _prefill_args(q, k_cache, v_cache, k_scale_cache, v_scale_cache, out, cu_seqlens_q, seqused_k,
+                                block_table, max_seqlen_q, softmax_scale, max_seqlen_k, num_splits)
+    # the reference multiplies the fp32 query by softmax_scale * LOG2E, which torch rounds to fp32 first
+    args.softmax_scale = float(np.float32(softmax_scale * LOG2E))
     lib = _hip.lib()
-    need = lib.qp_prefill_workspace_size(cache, args)
+    need = lib.qp_prefill_i8_workspace_size(cache, args)
     ws = torch.empty(need, dtype=torch.uint8, device=q.device) if need > 0 else None
     args.workspace = _hip.ptr(ws)
     args.workspace_bytes = need
-    _hip.check(lib.qp_prefill(cache, args, _hip.stream_of(q)), "prefill")
+    _hip.check(lib.qp_prefill_i8(cache, args, _hip.stream_of(q)), "prefill (int8 query split)")
 
 
 def prefill_sequence(q_rot, k_cache, v_cache, k_scales, v_scales, block_row, n, softmax_scale, fa=None):
@@ -113,7 +146,19 @@ def prefill_sequence(q_rot, k_cache, v_cache, k_scales, v_scales, block_row, n, 
 
 def prefill_sequence_i8(q_rot, k_cache, v_cache, k_scales, v_scales, block_row, n, softmax_scale, block_m=64,
                         block_n=64, num_warps=8, num_stages=2):
-    """The reference's single-kernel alternative with the same contract as prefill_sequence (int4_prefill.py:176-200);
-    its tile arguments are accepted and not used: the MFMA kernel serves both names, with the exact arithmetic."""
+    """The reference's single-kernel alternative (int4_prefill.py:176-200) with the same contract as
+    prefill_sequence, and its arithmetic (prefill_attention_i8): the int8 query split, int8 QK^T on the raw nibbles,
+    fp16 PV. Its Triton tile arguments are accepted and not used (the HIP kernel has its own tiles)."""
     del block_m, block_n, num_warps, num_stages
-    return prefill_sequence(q_rot, k_cache, v_cache, k_scales, v_scales, block_row, n, softmax_scale)
+    qlen = q_rot.shape[0]
+    q = q_rot if q_rot.dtype == torch.bfloat16 else q_rot.to(torch.bfloat16)
+    out = torch.empty_like(q)
+    dev = q.device
+    cu = _cu_seqlens(qlen, dev)
+    used = torch.full((1,), int(n), dtype=torch.int32, device=dev)
+    table = block_row.reshape(1, -1)
+    if table.dtype != torch.int32:
+        table = table.to(torch.int32)
+    prefill_attention_i8(q, k_cache, v_cache, k_scales, v_scales, out, cu_seqlens_q=cu, seqused_k=used,
+                         block_table=table, max_seqlen_q=qlen, softmax_scale=softmax_scale)
+    return out if q_rot.dtype == torch.bfloat16 else out.to(q_rot.dtype)

@@ -1,7 +1,9 @@
 """Time the chunked-prefill kernel on a named synthetic prefill workload (one MI355X).
 
     PYTHONPATH=vllm-quantpack_amd python -m vllm_quantpack.tools.time_prefill [--workload prefill-int4-128k-c1024] \
-        [--reps 5] [--splits N]
+        [--reps 5] [--splits N] [--i8]
+
+--i8 times the reference's single-kernel alternative arithmetic (qp_prefill_i8) instead of the exact one.
 
 The workload's chunk keys are stored into the cache first (as the benchmark does), then `reps` prefill calls run back
 to back between one event pair. Prints one JSON line with the average call time, the attention FLOPs of the chunk
@@ -28,6 +30,8 @@ def main(argv=None):
     ap.add_argument("--workload", default="prefill-int4-128k-c1024")
     ap.add_argument("--reps", type=int, default=5)
     ap.add_argument("--splits", type=int, default=0, help="key splits per query block (0: the library's choice)")
+    ap.add_argument("--i8", action="store_true",
+                    help="the reference's single-kernel alternative arithmetic (int8 query split, qp_prefill_i8)")
     args = ap.parse_args(argv)
 
     import torch
@@ -43,12 +47,13 @@ def main(argv=None):
                   k_scale_cache=d["k_scale_cache"], v_scale_cache=d["v_scale_cache"], rotate=False)
     out = torch.empty_like(d["q"])
 
+    fn = int4_prefill.prefill_attention_i8 if args.i8 else int4_prefill.prefill_attention
+
     def step():
-        int4_prefill.prefill_attention(d["q"], d["k_cache"], d["v_cache"], d["k_scale_cache"], d["v_scale_cache"],
-                                       out, cu_seqlens_q=d["cu_seqlens_q"], seqused_k=d["seqused_k"],
-                                       block_table=d["block_table"], max_seqlen_q=w.max_query_len,
-                                       softmax_scale=w.softmax_scale, max_seqlen_k=int(w.seqused_k.max()),
-                                       num_splits=args.splits)
+        fn(d["q"], d["k_cache"], d["v_cache"], d["k_scale_cache"], d["v_scale_cache"], out,
+           cu_seqlens_q=d["cu_seqlens_q"], seqused_k=d["seqused_k"], block_table=d["block_table"],
+           max_seqlen_q=w.max_query_len, softmax_scale=w.softmax_scale, max_seqlen_k=int(w.seqused_k.max()),
+           num_splits=args.splits)
 
     step()
     torch.cuda.synchronize()
@@ -62,7 +67,8 @@ def main(argv=None):
     ms = a.elapsed_time(b) / args.reps
     flops = chunk_flops(w)
     tflops = flops / (ms * 1e-3) / 1e12
-    print(json.dumps({"workload": args.workload, "reps": args.reps, "ms": round(ms, 4), "flops": flops,
+    print(json.dumps({"workload": args.workload, "kernel": "qp_prefill_i8" if args.i8 else "qp_prefill",
+                      "reps": args.reps, "ms": round(ms, 4), "flops": flops,
                       "tflops": round(tflops, 1), "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
                       "tok_s": round(w.q.shape[0] / (ms * 1e-3), 1)}), flush=True)
     return 0
