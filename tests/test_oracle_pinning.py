@@ -20,6 +20,11 @@
 | round_half_away          | known answers incl. fp32 `x + 0.5` rounding                                                 |
 | rht                      | R R^T = hs I, Sylvester entries (-1)^popcount(i & j), pure-Python hash of the signs          |
 | prefill_dequant_attend   | fp64 attention within 1e-2                                                                  |
+| quantize_query_i8        | hand rows (half to even, the 1e-20 floor), the reconstruction bound, torch running the       |
+|                          | reference's own lines (int4_prefill.py:181-189) bit for bit                                 |
+| i8_scores                | term-by-term brute force of the integer dots and the two fp32 products                     |
+| prefill_i8_emulated      | fp64 within 0.2 %; four planted mistakes (hi part alone, no key / value zero point, the     |
+|                          | query sum weighted 256) each fail it                                                        |
 """
 import numpy as np
 import pytest
