@@ -32,6 +32,7 @@ def hipcc():
 # Per-source extra flags. The prefill kernel keeps its QK^T MFMA results in VGPRs (its PV accumulators own the AGPRs).
 # The decode kernels take no NaN inputs (masked scores are -inf, never NaN), so their maxima need no quieting.
 EXTRA = {"qp_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+         "qp_prefill_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
          # the one atomic (a chunk claim by lane 0) needs no wave-level reduction around it
          "qp_decode.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]}
 
