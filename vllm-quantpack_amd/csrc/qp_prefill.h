@@ -63,7 +63,7 @@ struct PfShape {
   static constexpr int kVtRows = HS + 16;                    // + the zero-point tile
   static constexpr int kKd = kPfKeys * kKdRow;               // one K buffer
   static constexpr int kVt = kVtRows * kVtRow;
-  static constexpr int kKf = 3 * kPfKeys * 4 + 16;           // a_k, e_k, s_v + a dummy slot
+  static constexpr int kKf = 3 * kPfKeys * 4 + 16;           // a_k, e_k, b_k (bias log2(s_v) / a_k) + a dummy slot
   static constexpr int kVb = kVt + kKf;                      // one V buffer: V^T rows, then the per-key scalars
   static constexpr int kOffK = 3 * kPk;                      // 3 packed slots, 2 K buffers, 3 V buffers
   static constexpr int kOffV = kOffK + 2 * kKd;

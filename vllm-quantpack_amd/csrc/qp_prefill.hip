@@ -6,7 +6,11 @@
 // computes the exact kernel's arithmetic for any chunk length: bf16 query and exact-integer code operands, fp32
 // accumulation, S = (q . (128 + k) - sum(q) (128 + zp_k)) s_k scale for int4 keys and (q . (128 + k) - 128 sum(q))
 // s_k scale for int8 keys (both operands exact bf16 integers), P_v16 = bf16(P s_v) feeding both the PV product
-// and the zero-point sum (int4_kv.py:90-94), l from the unrounded P, causal within each sequence's query chunk.
+// and the zero-point sum (int4_kv.py:90-94), causal within each sequence's query chunk. Two steps differ in form:
+// P s_v is one exp2 of the score plus log2(s_v) (a per-key start value of the QK accumulator), and l is the sum of
+// P_v16 / s_v (two more rows of the zero-point tile hold 1 / s_v), where the reference sums the unrounded P. The
+// two l differ by the bf16 rounding of the weights, at most 2^-9 relative, and this l is the normaliser of the
+// weights the accumulator actually used.
 //
 // MI355X design. A workgroup of 4 waves (one per SIMD) owns (row block, KV head, key split). A row block is 64 NT
 // consecutive (token, query head) pairs of one sequence in token-major order, so any GQA width fills it, cut into
@@ -17,7 +21,8 @@
 //     issued four tiles ahead of the tile whose PV runs, from one scalar base per page run and fixed lane offsets;
 //   * all threads unpack the next tile to exact bf16 integers: K rows (128 + n, channel order permuted like the
 //     query operand), V^T rows (16 + n, keys in MFMA K-slot order) plus a 17th channel tile whose first row holds
-//     16 + zp_v, so the zero-point sum sum_k P16_k (16 + zp_v,k) comes out of the PV MFMA instead of the VALU. The
+//     16 + zp_v and whose next two rows hold 1 / s_v (two bf16 halves), so the zero-point sum
+//     sum_k P16_k (16 + zp_v,k) and l = sum_k P16_k / s_v,k come out of the PV MFMA instead of the VALU. The
 //     V offset is 16 rather than 128 because acc - sum P16 (offset + zp) cancels: over the tens of thousands of keys
 //     of one split, fp32 rounding of the offset-128 sums alone measured 0.5-0.9 % of the output;
 //   * each wave runs S^T = K Q^T (v_mfma_f32_16x16x32_bf16, K as the A operand), the softmax in registers and
@@ -40,6 +45,35 @@ namespace qp {
 
 // row_pos of a row past the block's last (token, head) pair: below every key, as a row without keys, but not stored
 constexpr int kPfNoRow = -0x7FFFFFFF - 1;
+
+// The per-key scalars of the softmax, from the key's and value's scale words:
+//   a = s_k scale log2(e) and e = a (128 + zp_k) (int8 keys: 128 a), so that the score is raw a - qsum e;
+//   b = log2(s_v) / a, the start value of the key's QK accumulator: the score then carries log2(s_v), and one exp2
+//     gives P s_v, the value probability, without a multiply;
+//   r = 1 / s_v as two bf16 halves (hi + lo, 16 bits), two rows of the zero-point tile: the PV MFMA then sums
+//     P16 / s_v, the row's l, without a VALU add per key.
+// A key past the split's end gets zeros. The store floors both scales at 1e-6, so a written key has a, s_v > 0; a
+// zero scale (never written) yields b = 0 and r = 0 rather than an infinity. b and r use v_rcp_f32 (about 1 ulp):
+// b's error then moves the score by about |log2 s_v| 2^-23 log2 units, and r is kept to 16 bits anyway.
+template <int KFMT>
+__device__ __forceinline__ void pf_key_scalars(uint32_t kw, uint32_t vw, float scale_log2, bool ok, float &a, float &e,
+                                               float &b, uint16_t &rhi, uint16_t &rlo) {
+  if constexpr (KFMT == QP_CODES_INT4) {
+    a = __uint_as_float(kw & 0xFFFFFFF0u) * scale_log2;
+    e = a * (float)(128u + (kw & 0xFu));
+  } else {
+    a = __uint_as_float(kw) * scale_log2;
+    e = a * 128.f;  // the operands are 128 + k
+  }
+  const float sv = __uint_as_float(vw & 0xFFFFFFF0u);
+  const bool fine = ok && sv > 0.f && a > 1e-30f;
+  b = fine ? __builtin_amdgcn_logf(sv) * __builtin_amdgcn_rcpf(a) : 0.f;
+  const float r = fine ? __builtin_amdgcn_rcpf(sv) : 0.f;
+  rhi = f32_to_bf16_bits(r);
+  rlo = f32_to_bf16_bits(r - __uint_as_float((uint32_t)rhi << 16));
+  a = ok ? a : 0.f;
+  e = ok ? e : 0.f;
+}
 
 // K part of the unpack: bf16 K rows kd[key][channel], 8 channels per dword of int4 codes (4 of int8).
 template <int HS, int KFMT>
@@ -103,28 +137,27 @@ __device__ __forceinline__ void pf_unpack_v(const uint8_t *pk, uint8_t *vt, int 
     const bool ok = k0 + kk < kend;
     const uint32_t kw = *reinterpret_cast<const uint32_t *>(pk + kk * Sh::kCell + Sh::kKeyBytes);
     const uint32_t vw = *reinterpret_cast<const uint32_t *>(pk + kk * Sh::kCell + Sh::kCell - 4);
-    float a, e;
-    if constexpr (KFMT == QP_CODES_INT4) {
-      a = __uint_as_float(kw & 0xFFFFFFF0u) * scale_log2;
-      e = a * (float)(128u + (kw & 0xFu));
-    } else {
-      a = __uint_as_float(kw) * scale_log2;
-      e = a * 128.f;  // the operands are 128 + k
-    }
+    float a, e, b;
+    uint16_t rhi, rlo;
+    pf_key_scalars<KFMT>(kw, vw, scale_log2, ok, a, e, b, rhi, rlo);
     float *kf = reinterpret_cast<float *>(vt + Sh::kVt);
-    kf[kk] = ok ? a : 0.f;
-    kf[kPfKeys + kk] = ok ? e : 0.f;
-    kf[2 * kPfKeys + kk] = ok ? __uint_as_float(vw & 0xFFFFFFF0u) : 0.f;
+    kf[kk] = a;
+    kf[kPfKeys + kk] = e;
+    kf[2 * kPfKeys + kk] = b;
     const int slot_off = 16 * ((kk & 15) >> 2) + 2 * ((kk & 3) + 4 * (kk >> 4));
     *reinterpret_cast<uint16_t *>(vt + HS * Sh::kVtRow + slot_off) = ok ? (uint16_t)(0x4180u | ((vw & 0xFu) << 3)) : 0;
+    *reinterpret_cast<uint16_t *>(vt + (HS + 1) * Sh::kVtRow + slot_off) = rhi;
+    *reinterpret_cast<uint16_t *>(vt + (HS + 2) * Sh::kVtRow + slot_off) = rlo;
   }
 }
 
 template <int HS, int NT>
 struct PfRows {
   bf16x8_t qop[NT][HS / 32];
-  f32x4_t acc[NT][17];  // O^T tiles: tile b row j -> channel 16 b + 4 g + j; tile HS/16 row 0 = zp sum (17 = 256 / 16 + 1)
-  float qsum[NT], m[NT], l[NT];
+  // O^T tiles: tile b register j -> channel 16 b + 4 g + j; in tile HS/16 (17 = 256 / 16 + 1), channel HS is the
+  // zero-point sum and channels HS + 1, HS + 2 the two halves of l
+  f32x4_t acc[NT][17];
+  float qsum[NT], m[NT];
   int row_pos[NT];  // the row's position in its sequence (< 0: a context shorter than the chunk), or kPfNoRow
 };
 
@@ -187,23 +220,21 @@ struct PfStager {
   __device__ __forceinline__ void s_store() {
     const int kk = tid & (kPfKeys - 1);
     const bool ok = full || k0 + kk < kend;
-    float a, e;
-    if constexpr (KFMT == QP_CODES_INT4) {
-      a = __uint_as_float(kw & 0xFFFFFFF0u) * scale_log2;
-      e = a * (float)(128u + (kw & 0xFu));
-    } else {
-      a = __uint_as_float(kw) * scale_log2;
-      e = a * 128.f;  // the operands are 128 + k
-    }
+    float a, e, b;
+    uint16_t rhi, rlo;
+    pf_key_scalars<KFMT>(kw, vw, scale_log2, ok, a, e, b, rhi, rlo);
     const bool own = tid < kPfKeys;
     float *kf = reinterpret_cast<float *>(vt + Sh::kVt);
     float *dummy = kf + 3 * kPfKeys;
-    *(own ? kf + kk : dummy) = ok ? a : 0.f;
-    *(own ? kf + kPfKeys + kk : dummy + 1) = ok ? e : 0.f;
-    *(own ? kf + 2 * kPfKeys + kk : dummy + 2) = ok ? __uint_as_float(vw & 0xFFFFFFF0u) : 0.f;
+    uint8_t *dummy16 = reinterpret_cast<uint8_t *>(dummy + 3);
+    *(own ? kf + kk : dummy) = a;
+    *(own ? kf + kPfKeys + kk : dummy + 1) = e;
+    *(own ? kf + 2 * kPfKeys + kk : dummy + 2) = b;
     const int slot_off = 16 * ((kk & 15) >> 2) + 2 * ((kk & 3) + 4 * (kk >> 4));
-    *reinterpret_cast<uint16_t *>(own ? vt + HS * Sh::kVtRow + slot_off : reinterpret_cast<uint8_t *>(dummy + 3)) =
+    *reinterpret_cast<uint16_t *>(own ? vt + HS * Sh::kVtRow + slot_off : dummy16) =
         ok ? (uint16_t)(0x4180u | ((vw & 0xFu) << 3)) : 0;
+    *reinterpret_cast<uint16_t *>(own ? vt + (HS + 1) * Sh::kVtRow + slot_off : dummy16) = rhi;
+    *reinterpret_cast<uint16_t *>(own ? vt + (HS + 2) * Sh::kVtRow + slot_off : dummy16) = rlo;
   }
 };
 
@@ -259,26 +290,36 @@ __device__ __forceinline__ void p_ready(u32x4_t (&pop)[NT]) {
 }
 
 // one QK step (32 channels of one 16-key sub-tile) for every row tile of the wave
+// (a sub-tile's first step starts from the keys' biases b = log2(s_v) / a, the same for every row)
 template <int HS, int NT>
 __device__ __forceinline__ void qk_step(f32x4_t (&d)[NT][2], int sub, int mi, bf16x8_t kop,
-                                        const bf16x8_t (&qop)[NT][HS / 32]) {
+                                        const bf16x8_t (&qop)[NT][HS / 32], const f32x4_t (&bias)[2]) {
 #pragma unroll
-  for (int j = 0; j < NT; ++j)
-    d[j][sub] = mfma16x16x32(kop, qop[j][mi], mi == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : d[j][sub]);
+  for (int j = 0; j < NT; ++j) d[j][sub] = mfma16x16x32(kop, qop[j][mi], mi == 0 ? bias[sub] : d[j][sub]);
+}
+
+// the biases of this lane's four keys of each sub-tile (lane group g holds keys 16 sub + 4 g + jj)
+template <class Sh>
+__device__ __forceinline__ void load_bias(const uint8_t *vb, int g, f32x4_t (&bias)[2]) {
+  const float *kf = reinterpret_cast<const float *>(vb + Sh::kVt);
+#pragma unroll
+  for (int sb = 0; sb < 2; ++sb) bias[sb] = *reinterpret_cast<const f32x4_t *>(kf + 2 * kPfKeys + 16 * sb + 4 * g);
 }
 
 // S^T of one tile for all row tiles of the wave (prologue of a pass).
 template <int HS, int KFMT, int NT>
-__device__ __forceinline__ void pf_qk_tile(const PfRows<HS, NT> &r, const uint8_t *kd, f32x4_t (&sacc)[NT][2],
-                                           int col, int g) {
+__device__ __forceinline__ void pf_qk_tile(const PfRows<HS, NT> &r, const uint8_t *kd, const uint8_t *vb,
+                                           f32x4_t (&sacc)[NT][2], int col, int g) {
   using Sh = PfShape<HS, KFMT>;
+  f32x4_t bias[2];
+  load_bias<Sh>(vb, g, bias);
 #pragma unroll
   for (int sub = 0; sub < 2; ++sub) {
     const uint8_t *kr = kd + (16 * sub + col) * Sh::kKdRow + 16 * Sh::kd_unit((HS / 32) * g);
 #pragma unroll
     for (int mi = 0; mi < HS / 32; ++mi) {
       const bf16x8_t kop = *reinterpret_cast<const bf16x8_t *>(kr + 16 * mi);
-      qk_step<HS, NT>(sacc, sub, mi, kop, r.qop);
+      qk_step<HS, NT>(sacc, sub, mi, kop, r.qop, bias);
     }
   }
 }
@@ -324,7 +365,7 @@ __device__ __forceinline__ void pf_initial_max(PfRows<HS, NT> &r, const f32x4_t 
 // of an LDS region no wave reads during phase A), and the tile's probabilities are taken against the new maximum.
 template <int HS, int KFMT, int NT, bool MASK>
 __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev)[NT][2], f32x4_t (&snew)[NT][2],
-                                        const uint8_t *kd1, const uint8_t *vb0, int k0, int kend,
+                                        const uint8_t *kd1, const uint8_t *vb0, const uint8_t *vb1, int k0, int kend,
                                         f32x4_t *rescale_lds, PfStager<HS, KFMT> &st, int col, int g) {
   using Sh = PfShape<HS, KFMT>;
   using St = PfStager<HS, KFMT>;
@@ -346,7 +387,8 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
   };
   auto vaddr = [&](int b) { return vb0 + (16 * b + col) * Sh::kVtRow + 16 * g; };
   bf16x8_t kbuf[kPre], vbuf[kPreV];
-  float4 ka[2], ke[2], ks[2];
+  float4 ka[2], ke[2];
+  f32x4_t bias[2];  // tile i + 1's keys, for its QK
   float t[NT][2][4];
   u32x4_t pop[NT];
 
@@ -375,7 +417,6 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
         const float up = rm > kPfRescale ? rm : 0.f;
         r.m[j] += up;
         const float alpha = __builtin_amdgcn_exp2f(-up);
-        r.l[j] *= alpha;
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
@@ -384,10 +425,10 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
       }
     } else {
       const int sub = (k - 3) >> 1, h2 = (k - 3) & 1;
+      // the scores carry log2(s_v): these are P s_v (l comes out of the PV MFMA)
       const float p0 = __builtin_amdgcn_exp2f(t[j][sub][2 * h2]);
       const float p1 = __builtin_amdgcn_exp2f(t[j][sub][2 * h2 + 1]);
-      r.l[j] += p0 + p1;  // after any rescale of l in item 2
-      pop[j][2 * sub + h2] = pack_bf16x2(p0 * ks[sub][2 * h2], p1 * ks[sub][2 * h2 + 1]);
+      pop[j][2 * sub + h2] = pack_bf16x2(p0, p1);
     }
   };
 
@@ -398,14 +439,14 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
   for (int sb = 0; sb < 2; ++sb) {
     ka[sb] = *reinterpret_cast<const float4 *>(kf + 16 * sb + 4 * g);
     ke[sb] = *reinterpret_cast<const float4 *>(kf + kPfKeys + 16 * sb + 4 * g);
-    ks[sb] = *reinterpret_cast<const float4 *>(kf + 2 * kPfKeys + 16 * sb + 4 * g);
   }
+  load_bias<Sh>(vb1, g, bias);
 #pragma unroll
   for (int s = 0; s < kQ; ++s) {
     const int sub = s / kMi, mi = s % kMi;
     const bf16x8_t kop = kbuf[s % kPre];
     if (s + kPre < kQ) kbuf[s % kPre] = *reinterpret_cast<const bf16x8_t *>(kaddr(s + kPre));
-    qk_step<HS, NT>(snew, sub, mi, kop, r.qop);
+    qk_step<HS, NT>(snew, sub, mi, kop, r.qop, bias);
     // each K unit's store follows its load by kLag steps, so at most kLag + 1 units are held (int8 keys have 8)
     if (s < St::kNK) st.k_load(s);
     if (s >= kLag && s < St::kNK + kLag) st.k_store(s - kLag);
@@ -588,7 +629,6 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
   // raised in place (l and the accumulators scaled down) when a tile's scores exceed it by more than the headroom.
 #pragma unroll
   for (int jt = 0; jt < NT; ++jt) {
-    r.l[jt] = 0.f;
 #pragma unroll
     for (int b = 0; b <= HS / 16; ++b) r.acc[jt][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
@@ -616,7 +656,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
       pf_unpack_v<HS, KFMT>(pk_of(1), vb_of(1), tile_key(1), ke, p.scale_log2, tid);
     }
     f32x4_t sprev[NT][2], snew[NT][2];
-    pf_qk_tile<HS, KFMT, NT>(r, kd_of(0), sprev, col, g);
+    pf_qk_tile<HS, KFMT, NT>(r, kd_of(0), vb_of(0), sprev, col, g);
     pf_initial_max<HS, KFMT, NT>(r, sprev, vb_of(0), tile_key(0), ke, tile_key(0) + kPfKeys > vis_all, g);
 
     // block ids of tile 4, fetched a tile ahead of its copy through the scalar cache (constant address space: the
@@ -689,7 +729,8 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
       st.kend = ke;
       st.tid = tid;
       st.scale_log2 = p.scale_log2;
-      pf_iter<HS, KFMT, NT, kMask>(r, sprev, snew, kd_at(1), vb_at(0), tile_key(it), ke, rescale_slot, st, col, g);
+      pf_iter<HS, KFMT, NT, kMask>(r, sprev, snew, kd_at(1), vb_at(0), vb_at(1), tile_key(it), ke, rescale_slot, st,
+                                   col, g);
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         sprev[j][0] = snew[j][0];
@@ -721,13 +762,11 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
     if constexpr (SPAN) wait_vmcnt<0>();
   }
 
-  // ---- epilogue: l over the 4 lane groups, zero-point sum from the extra tile, store
+  // ---- epilogue: zero-point sum and l from the extra tile (lane group 0), store
 #pragma unroll
   for (int jt = 0; jt < NT; ++jt) {
-    float l = r.l[jt];
-    l += shfl_xor_f(l, 16);
-    l += shfl_xor_f(l, 32);
     const float csum = __shfl(r.acc[jt][HS / 16][0], col, 64);
+    const float l = __shfl(r.acc[jt][HS / 16][1] + r.acc[jt][HS / 16][2], col, 64);
     const bool valid = r.row_pos[jt] != kPfNoRow;  // the same for the four lanes of a row (lanes col + 16 g)
     // the row's token from its position (live for the mask), its head without a division
     const int tl = valid ? r.row_pos[jt] - (n - qlen) : 0;
