@@ -28,9 +28,11 @@
 //   * each wave runs S^T = K Q^T (v_mfma_f32_16x16x32_bf16, K as the A operand), the softmax in registers and
 //     O^T += V^T P^T with P^T straight from the S^T registers.
 // The unpack of tile i + 2 sits in the same basic blocks as the QK MFMAs of tile i + 1 and the PV MFMAs of tile i,
-// so the scheduler interleaves them. With one wave per SIMD only about one VALU instruction per 16-cycle MFMA comes
-// free (measured marginal costs of about 1, 2, 3 and 4.5 cycles for the first to the fourth), so the VALU count per
-// tile sets much of the time.
+// so a scheduler can interleave them. With one wave per SIMD an MFMA takes about 9 of its 16 pipe cycles of the
+// wave's issue, so about 7 cycles of other work (one or two VALU ops) come free behind each one (measured:
+// max(16.6, 9 + 4 N) cycles per MFMA with N FMAs after it). The build orders these blocks with its own post-RA
+// scheduler (mirsched.py), which fills that shadow where LLVM's order runs MFMAs back to back; the VALU count per
+// tile still sets much of the time.
 // The running maximum is raised lazily: a tile rescales only when one of its scores exceeds the maximum by more than
 // kPfRescale (64 in log2 units), so the common path spends 2 VALU ops on a score instead of 3 plus a row reduction.
 // Probabilities are then relative to a maximum that may trail the true one by up to 2^64, far inside fp32's range,
@@ -251,31 +253,14 @@ __device__ __forceinline__ void pv_step(f32x4_t (&acc)[NT][17], int b, bf16x8_t 
                                         bool last) {
   static_assert(NT >= 1 && NT <= 3, "row tiles");
   // (the accumulator array is sized for head 256; head 128 uses tiles 0..8)
-  if constexpr (NT == 1) {
-    if (last)
+  // One statement per MFMA, so that VALU work can be placed between them; the tile's last carries the wait states.
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    if (last && j == NT - 1)
       asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 1"
-                   : "+a"(acc[0][b]) : "v"(vop), "v"(pop[0]));
+                   : "+a"(acc[j][b]) : "v"(vop), "v"(pop[j]));
     else
-      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc[0][b]) : "v"(vop), "v"(pop[0]));
-  } else if constexpr (NT == 2) {
-    if (last)
-      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %2, %3, %0\n\tv_mfma_f32_16x16x32_bf16 %1, %2, %4, %1\n\t"
-                   "s_nop 7\n\ts_nop 7\n\ts_nop 1"
-                   : "+a"(acc[0][b]), "+a"(acc[1][b]) : "v"(vop), "v"(pop[0]), "v"(pop[1]));
-    else
-      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %2, %3, %0\n\tv_mfma_f32_16x16x32_bf16 %1, %2, %4, %1"
-                   : "+a"(acc[0][b]), "+a"(acc[1][b]) : "v"(vop), "v"(pop[0]), "v"(pop[1]));
-  } else {
-    if (last)
-      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %3, %4, %0\n\tv_mfma_f32_16x16x32_bf16 %1, %3, %5, %1\n\t"
-                   "v_mfma_f32_16x16x32_bf16 %2, %3, %6, %2\n\ts_nop 7\n\ts_nop 7\n\ts_nop 1"
-                   : "+a"(acc[0][b]), "+a"(acc[1][b]), "+a"(acc[2][b])
-                   : "v"(vop), "v"(pop[0]), "v"(pop[1]), "v"(pop[2]));
-    else
-      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %3, %4, %0\n\tv_mfma_f32_16x16x32_bf16 %1, %3, %5, %1\n\t"
-                   "v_mfma_f32_16x16x32_bf16 %2, %3, %6, %2"
-                   : "+a"(acc[0][b]), "+a"(acc[1][b]), "+a"(acc[2][b])
-                   : "v"(vop), "v"(pop[0]), "v"(pop[1]), "v"(pop[2]));
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc[j][b]) : "v"(vop), "v"(pop[j]));
   }
 }
 
