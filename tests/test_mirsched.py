@@ -74,13 +74,14 @@ def test_instruction_operands():
     i = ms.Inst(inline_mfma(200, 50, 60))
     assert i.kind == "mfma" and i.mfmas == 1 and not i.mem and not i.trailing_waits
     assert i.defs == {f"a{r}" for r in range(200, 204)}
-    assert i.uses == {f"a{r}" for r in range(200, 204)} | {f"v{r}" for r in range(50, 54)} | {f"v{r}" for r in range(60, 64)}
+    assert i.uses == ({f"a{r}" for r in range(200, 204)} | {f"v{r}" for r in range(50, 54)} |
+                      {f"v{r}" for r in range(60, 64)} | {"exec_lo", "exec_hi"})
     assert ms.Inst(inline_mfma(200, 50, 60, nops=True)).trailing_waits
     i = ms.Inst('INLINEASM &"s_mov_b32 m0, $2\\0A\\09s_nop 0\\0A\\09global_load_lds_dwordx4 $0, $1", 57 /* sideeffect '
                 'mayload maystore isconvergent attdialect */, 1835017 /* reguse:VGPR_32 */, killed renamable $vgpr0, '
                 '5242889 /* reguse:SGPR_64 */, renamable $sgpr2_sgpr3, 2424841 /* reguse:SReg_32 */, killed renamable '
                 '$sgpr7, 12 /* clobber */, implicit-def early-clobber $m0')
-    assert i.mem and i.defs == {"m0"} and i.uses == {"v0", "s2", "s3", "s7"}
+    assert i.mem and i.defs == {"m0"} and i.uses == {"v0", "s2", "s3", "s7", "exec_lo", "exec_hi"}
     i = ms.Inst("renamable $sgpr12 = S_ADD_U32 renamable $sgpr73, killed renamable $sgpr10, implicit-def $scc")
     assert i.kind == "salu" and i.defs == {"s12", "scc"} and i.uses == {"s73", "s10"} and not i.mem
     assert ms.Inst("S_BARRIER").mem and ms.Inst("ATOMIC_FENCE 5, 2").mem
@@ -125,6 +126,20 @@ def test_inline_mfma_with_wait_states_stays_last():
     order = [x.text for x in ms.schedule(insts)]
     last = order.index(block[2])
     assert order.index(block[0]) < last and order.index(block[1]) < last and order.index(block[5]) > last
+
+
+def test_inline_assembly_stays_on_its_side_of_exec_writes():
+    """A lane-masked copy region (s_and_saveexec ... branch): neither an LDS-DMA copy nor an inline MFMA written
+    before the EXEC write may move below it (they would run on the narrowed mask)."""
+    dma = ('INLINEASM &"s_mov_b32 m0, $2\\0A\\09s_nop 0\\0A\\09global_load_lds_dwordx4 $0, $1", 57 /* sideeffect '
+           'mayload maystore isconvergent attdialect */, 1835017 /* reguse:VGPR_32 */, renamable $vgpr219, '
+           '5242889 /* reguse:SGPR_64 */, renamable $sgpr52_sgpr53, 2424841 /* reguse:SReg_32 */, renamable $sgpr0, '
+           '12 /* clobber */, implicit-def early-clobber $m0')
+    save = "$sgpr64_sgpr65 = S_AND_SAVEEXEC_B64 $sgpr68_sgpr69, implicit-def $exec, implicit-def $scc, implicit $exec"
+    block = [inline_mfma(0, 50, 60), inline_mfma(4, 50, 64), dma, save, "S_CBRANCH_EXECZ %bb.9, implicit $exec"]
+    order = [x.text for x in ms.schedule([ms.Inst(t) for t in block])]
+    assert order.index(save) > max(order.index(block[0]), order.index(block[1]), order.index(dma))
+    assert "exec_lo" in ms.Inst(inline_mfma(0, 50, 60)).uses
 
 
 def test_valu_fills_the_mfma_shadow():

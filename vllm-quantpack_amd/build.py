@@ -42,9 +42,12 @@ EXTRA = {"qp_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 
 # Sources whose kernels (function names matching the pattern) go through the post-RA MFMA/VALU interleaving
 # scheduler (mirsched.py): their device code is compiled to LLVM MIR, stopped after LLVM's post-RA scheduler,
-# reordered, and finished by LLVM (wait counts, hazard wait states, emission). Measured on the 1024-token prefill
-# chunk over 131072 keys: 2.94-3.02 ms against 3.13 ms for the same source in LLVM's order.
-SCHEDULED = {"qp_prefill.hip": r"^_ZN2qp14prefill_kernel"}
+# reordered, and finished by LLVM (wait counts, hazard wait states, emission). Measured on 1024-token prefill chunks
+# over 131072 keys: the tile kernel 2.94-3.02 ms against 3.13 ms in LLVM's order, the wide kernel 6.28-6.30 against
+# 6.50-6.52 ms (head 128, 64 / 8 heads) and 4.89-4.92 against 5.01-5.03 ms (head 512). The decode kernel measured
+# slower scheduled (33.9-34.8 against 31.9-32.2 us) and the int8 alternative within 1 %, so they keep LLVM's order.
+SCHEDULED = {"qp_prefill.hip": r"^_ZN2qp14prefill_kernel",
+             "qp_prefill_wide.hip": r"^_ZN2qp19prefill_wide_kernel"}
 
 
 def _flags(src):

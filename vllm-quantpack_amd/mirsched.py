@@ -22,6 +22,8 @@ remaining path whose operands are ready fills the issue slots. Dependences:
   * memory and side effects: every instruction that is not a plain register-to-register ALU operation (loads,
     stores, LDS accesses, barriers, waits, fences, inline assembly that touches memory, wait counters or exec) keeps
     its order relative to all the others of that kind;
+  * inline assembly reads EXEC (its vector instructions run under it, though the statement does not list it), so
+    it never moves across an EXEC write such as a lane-masked region's s_and_saveexec;
   * inline-assembly MFMAs (invisible to LLVM's hazard recognizer): one that carries trailing wait states stays after
     every earlier inline MFMA of its block, and no later one moves above it, so the wait states still follow the
     last of them;
@@ -117,6 +119,8 @@ class Inst:
             operands = text.split('"', 2)[2] if text.count('"') >= 2 else text
             for m in re.finditer(r"(implicit-def|implicit|def)?\s*(?:" + _MODIFIERS + r")*(\$[A-Za-z0-9_]+)", operands):
                 (self.defs if m.group(1) in ("def", "implicit-def") else self.uses).update(reg_units(m.group(2)))
+            # vector instructions inside run under EXEC, which the statement does not list: never across its writes
+            self.uses |= {"exec_lo", "exec_hi"}
             self.mem = any(k in self.asm for k in _ASM_MEMORY)
         else:
             self._implicit(rhs)
@@ -308,7 +312,10 @@ def _instructions(lines, h, j):
 def schedule_mir(text, pattern):
     """The MIR text with every MFMA-holding block of the functions matching `pattern` rescheduled; returns (text,
     number of blocks rescheduled). Kill flags are dropped from moved blocks (the order they described changed)."""
-    lines = text.split("\n")
+    # The register scavenger's frame index is stale once prologue/epilogue insertion has lowered the frame (before
+    # this point), and this LLVM's MIR parser rejects it when it names a stack object listed after it: drop it (the
+    # round trip then reproduces LLVM's code exactly, spill code included).
+    lines = [l for l in text.split("\n") if not re.match(r"^  scavengeFI:\s+'%stack\.\d+'\s*$", l)]
     repl = []
     for s, e in _function_ranges(lines, pattern):
         for h, j in _blocks(lines, s, e):
