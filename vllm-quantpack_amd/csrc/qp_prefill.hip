@@ -358,9 +358,11 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
   constexpr int kQ = 2 * kMi;      // K operands per tile
   constexpr int kP = HS / 16 + 1;  // V^T operands (channel tiles + the zero-point tile)
   // Operand loads ahead: 4 for the 16 K operands (a divisor, so the rotating registers line up with the tile and no
-  // copies are needed: 18 fewer VALU per tile than 3, which measured 3.69 against 3.77 ms), 3 for the 17 V^T ones.
+  // copies are needed: 18 fewer VALU per tile than 3, which measured 3.69 against 3.77 ms), 6 for the 17 V^T ones
+  // (with the build's scheduler interleaving the PV steps: 2.92-2.94 ms against 2.98-3.08 for 3 on the 1024-token
+  // chunk over 131072 keys, k8v4 3.48 against 3.53-3.62 ms; 4 and 5 in between; the same registers).
   constexpr int kPre = 4;
-  constexpr int kPreV = 3;
+  constexpr int kPreV = 6;
   constexpr int kSm = 7;           // softmax work items per row tile
   constexpr int kLag = St::kNK < 4 ? St::kNK : 4;
   static_assert(St::kNK + kLag <= kQ, "K unpack stages must fit phase A");
