@@ -14,7 +14,8 @@ from qp_testlib import assert_emulation, to_f32
 
 DECODE = ["decode-int4-4k-t1", "decode-int4-128k-t2", "decode-int4-256k-t4", "decode-k8v4-ragged-b32"]
 PREFILL = ["prefill-int4-128k-c1024", "prefill-k8v4-128k-c1024", "prefill-int4-h512-128k-c1024",
-           "prefill-int4-g16-32k-c1024", "prefill-int4-g8-128k-c1024"]
+           "prefill-int4-g16-32k-c1024", "prefill-int4-g8-128k-c1024",
+           "prefill-int4-g4-128k-c1024"]
 SEGMENTS = 64
 
 

@@ -14,6 +14,8 @@ Workloads (24 query / 4 KV heads, head 256, block 16 unless stated):
                            per KV head), head 256
   prefill-int4-g8-128k-c1024  the prefill chunk workload with 64 query / 8 KV heads at head 128 (the attention of a
                            Llama-3-70B-class layer on one GPU: 8 query heads per KV head)
+  prefill-int4-g4-128k-c1024  the prefill chunk workload with 32 query / 8 KV heads at head 128 (a Llama-3-8B or
+                           Mistral-7B-class layer: 4 query heads per KV head)
 
 int4 cells: nibbles uniform 0..15; per (token, KV head) fp32 scale ~ lognormal(-3, 0.5) with its low 4 mantissa bits
 replaced by the zero point round(U(6, 9)). k8v4 keys: int8 uniform -127..127, fp32 scale ~ lognormal(-4, 0.5).
@@ -29,7 +31,7 @@ NQ, NKV, HS, BS = 24, 4, 256, 16
 
 WORKLOADS = ("decode-int4-4k-t1", "decode-int4-128k-t2", "decode-int4-256k-t4", "prefill-int4-128k-c1024",
              "decode-k8v4-ragged-b32", "prefill-k8v4-128k-c1024", "prefill-int4-h512-128k-c1024",
-             "prefill-int4-g16-32k-c1024", "prefill-int4-g8-128k-c1024")
+             "prefill-int4-g16-32k-c1024", "prefill-int4-g8-128k-c1024", "prefill-int4-g4-128k-c1024")
 
 
 @dataclass
@@ -129,9 +131,9 @@ def make(name: str, *, small: bool = False) -> Workload:
     if name == "decode-int4-256k-t4":
         return _single(name, rng, 262144 // div, 4)
     if name in ("prefill-int4-128k-c1024", "prefill-k8v4-128k-c1024", "prefill-int4-h512-128k-c1024",
-                "prefill-int4-g16-32k-c1024", "prefill-int4-g8-128k-c1024"):
+                "prefill-int4-g16-32k-c1024", "prefill-int4-g8-128k-c1024", "prefill-int4-g4-128k-c1024"):
         k8v4 = name.startswith("prefill-k8v4")
-        shapes = {"-h512-": (16, 2, 512), "-g16-": (32, 2, HS), "-g8-": (64, 8, 128)}
+        shapes = {"-h512-": (16, 2, 512), "-g16-": (32, 2, HS), "-g8-": (64, 8, 128), "-g4-": (32, 8, 128)}
         nq, nkv, hs = next((v for k, v in shapes.items() if k in name), (NQ, NKV, HS))
         cached, chunk = (32768 if "-32k-" in name else 131072) // div, 1024 // (4 if small else 1)
         n = cached + chunk
