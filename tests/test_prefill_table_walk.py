@@ -1,10 +1,11 @@
 """The block-table entries the MFMA prefill kernels read with 16-token blocks, walked on the CPU.
 
 prefill_kernel (csrc/qp_prefill.hip) and prefill_wide_kernel (csrc/qp_prefill_wide.hip) read the table pair of tile
-t + 5 one iteration ahead of its copies, through a pointer that steps two entries per tile. Their steady iterations
-(the tile kernel's six-phase unrolled loop of int4 keys and rolled steady loop of int8 keys, the wide kernel's steady
-loop) take the pair's second entry without checking the split's end, which is only valid when that tile is followed by
-another one. This walk restates each kernel's loop structure (prologue and loops, with the `kPfSteadyLead` bound read
+t + 5 one iteration ahead of its copies, through a pointer that steps two entries per tile; the tile kernel's
+six-phase unrolled loop of int4 keys reads the 12 entries of tiles it + 5 .. it + 10 at once, in its first iteration.
+Their steady iterations (that unrolled loop, the tile kernel's rolled steady loop of int8 keys, the wide kernel's
+steady loop) take a pair's second entry without checking the split's end, which is only valid when that tile is
+followed by another one. This walk restates each kernel's loop structure (prologue and loops, with the `kPfSteadyLead` bound read
 from the source) and checks, for every context length mod 32, row blocks of (token, head) pairs at several GQA widths
 and the key-split geometry the kernels use, that
 
@@ -29,7 +30,10 @@ def steady_lead() -> int:
     m = re.search(r"constexpr int kPfSteadyLead = (\d+);", (CSRC / "qp_prefill.h").read_text())
     assert m, "kPfSteadyLead not found in qp_prefill.h"
     # both kernels bound their steady loops by it (the tile kernel's unrolled loop by it + 5 + kPfSteadyLead)
-    assert "it + 5 + kPfSteadyLead <= ntiles" in (CSRC / "qp_prefill.hip").read_text()
+    src = (CSRC / "qp_prefill.hip").read_text()
+    assert "it + 5 + kPfSteadyLead <= ntiles" in src
+    # the unrolled loop's group read, as walked below
+    assert "for (int k = 0; k < 12; ++k) tb[k] = tnext[k];" in src and "tnext += 12;" in src
     assert "it + kPfSteadyLead <= ntiles" in (CSRC / "qp_prefill_wide.hip").read_text()
     return int(m.group(1))
 
@@ -81,8 +85,12 @@ def walk(n, qlen, t_first, t_last, split, splits, int4, lead, wide=False):
     else:
         if int4:
             while it + 6 <= nplain and it + 5 + lead <= ntiles:
-                for k in range(6):
-                    iteration(it + k, True)
+                # iteration it reads tnext .. tnext + 11 in one load: the pairs of tiles it + 5 .. it + 10
+                assert state["next_tile"] == it + 5
+                tn = state["tnext"]
+                reads.extend((it + 5 + k // 2, tn + k) for k in range(12))
+                state["tnext"] += 12
+                state["next_tile"] += 6
                 it += 6
         else:
             while it < nplain and it + lead <= ntiles:
