@@ -371,8 +371,8 @@ __device__ __forceinline__ void table_pair(const int32_t *trow, int i0, int i1, 
 // between the AGPRs and LDS only inside assembly blocks (LDS loads and stores take AGPR data): any C++ access to an
 // element makes the register allocator keep a VGPR copy of every tile and refresh it at each chunk, although the
 // rescale runs only a few times per segment. Callers run it at least 18 wait states after the last accumulation into
-// the tiles (the last inline MFMA of a chunk ends with them); the lgkm wait at its end completes the reload before any
-// later MFMA reads a tile.
+// the tiles (the last inline MFMA of a decode or int8-prefill chunk ends with them; the tile prefill issues them
+// before the call); the lgkm wait at its end completes the reload before any later MFMA reads a tile.
 template <int N, int USED = N>
 __device__ __forceinline__ void scale_agpr(f32x4_t (&acc)[N], float alpha, f32x4_t *rs) {
   // an LDS-typed pointer: the round trip is ds_read / ds_write on a 32-bit address, not flat accesses

@@ -245,23 +245,31 @@ struct PfStager {
 // accumulators (NT x 17 tiles, up to 204 registers) must stay in AGPRs, and the compiler keeps them there only when
 // nothing else competes for that file: PV therefore runs as inline-assembly MFMAs with AGPR operands (pv_step), which
 // only other PV MFMAs touch until the epilogue. The compiler cannot see those as MFMAs; their results are read by
-// the next accumulation of the same tile (ordered by the hardware) and, after the last tile, by the epilogue, so the
-// last PV step of every tile ends with 18 wait states (an 8-pass XDL result needs 11 before any other read). The build
-// scans the generated code for any access to an MFMA destination within 18 wait states and fails if it finds one.
+// the next accumulation of the same tile (ordered by the hardware), by a rescale and, after the last tile, by the
+// epilogue. An 8-pass XDL result needs 11 wait states before any other read: the rescale and the epilogue start with
+// 18 (pv_drain), and the next tile's accumulations come after a barrier, the tile's copies and its first QK steps.
+// The PV steps themselves carry none: 18 at the end of every tile measured 1.7 % slower on the 1024-token chunk over
+// 131072 keys, as they sat just before the barrier. The build scans the generated code for any access to an MFMA
+// destination within 18 wait states and fails if it finds one.
 template <int NT>
-__device__ __forceinline__ void pv_step(f32x4_t (&acc)[NT][17], int b, bf16x8_t vop, const u32x4_t (&pop)[NT],
-                                        bool last) {
+__device__ __forceinline__ void pv_step(f32x4_t (&acc)[NT][17], int b, bf16x8_t vop, const u32x4_t (&pop)[NT]) {
   static_assert(NT >= 1 && NT <= 3, "row tiles");
   // (the accumulator array is sized for head 256; head 128 uses tiles 0..8)
-  // One statement per MFMA, so that VALU work can be placed between them; the tile's last carries the wait states.
+  // One statement per MFMA, so that VALU work can be placed between them.
 #pragma unroll
-  for (int j = 0; j < NT; ++j) {
-    if (last && j == NT - 1)
-      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 1"
-                   : "+a"(acc[j][b]) : "v"(vop), "v"(pop[j]));
-    else
-      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc[j][b]) : "v"(vop), "v"(pop[j]));
-  }
+  for (int j = 0; j < NT; ++j)
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc[j][b]) : "v"(vop), "v"(pop[j]));
+}
+
+// 18 wait states after the last PV MFMA, before code that reads the accumulators (the epilogue). The empty statements
+// pass every tile through after the wait states, so no read of a tile can be placed above them.
+template <int HS, int NT>
+__device__ __forceinline__ void pv_drain(f32x4_t (&acc)[NT][17]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 1" ::: "memory");
+#pragma unroll
+  for (int j = 0; j < NT; ++j)
+#pragma unroll
+    for (int b = 0; b <= HS / 16; ++b) asm volatile("" : "+a"(acc[j][b]));
 }
 
 // Two wait states between the VALU instructions that packed the P operands and the first PV MFMA reading them (the
@@ -396,8 +404,10 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
         }
       }
     } else if (k == 2) {
-      const float mx = fmaxf(fmaxf(fmaxf(t[j][0][0], t[j][0][1]), fmaxf(t[j][0][2], t[j][0][3])),
-                             fmaxf(fmaxf(t[j][1][0], t[j][1][1]), fmaxf(t[j][1][2], t[j][1][3])));
+      // a chain of three-input maxima: 4 instructions for the 8 scores
+      const float x = fmaxf(fmaxf(t[j][0][0], t[j][0][1]), t[j][0][2]);
+      const float y = fmaxf(fmaxf(t[j][0][3], t[j][1][0]), t[j][1][1]);
+      const float mx = fmaxf(fmaxf(fmaxf(x, y), t[j][1][2]), t[j][1][3]);
       if (__builtin_expect(__any(mx > kPfRescale), 0)) {
         float rm = fmaxf(mx, shfl_xor_f(mx, 16));  // the row's maximum over the tile (row = lane column)
         rm = fmaxf(rm, shfl_xor_f(rm, 32));
@@ -408,6 +418,7 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
         for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) t[j][sb][jj] -= up;
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 1" ::: "memory");  // the last PV MFMA's wait states
         scale_agpr<17, HS / 16 + 1>(r.acc[j], alpha, rescale_lds);
       }
     } else {
@@ -453,7 +464,7 @@ __device__ __forceinline__ void pf_iter(PfRows<HS, NT> &r, const f32x4_t (&sprev
   for (int b = 0; b < kP; ++b) {
     const bf16x8_t vop = vbuf[b % kPreV];
     if (b + kPreV < kP) vbuf[b % kPreV] = *reinterpret_cast<const bf16x8_t *>(vaddr(b + kPreV));
-    pv_step<NT>(r.acc, b, vop, pop, b == kP - 1);
+    pv_step<NT>(r.acc, b, vop, pop);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       if (at(b, q)) st.v_load(q);
@@ -765,6 +776,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(const PrefillPar
     for (; it < nplain; ++it) iteration(it, std::false_type{}, Unknown{});
     for (; it < ntiles; ++it) iteration(it, std::true_type{}, Unknown{});
     if constexpr (SPAN) wait_vmcnt<0>();
+    pv_drain<HS, NT>(r.acc);
   }
 
   // ---- epilogue: zero-point sum and l from the extra tile (lane group 0), store
