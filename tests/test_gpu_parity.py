@@ -682,6 +682,37 @@ def test_prefill_loop_boundaries(device, fmt, bs, splits):
         at += 20
 
 
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+@pytest.mark.parametrize("splits", [1, 0])
+def test_prefill_repeats_bit_for_bit(device, fmt, splits):
+    """The same call five times gives the same bits. Nothing in the kernels depends on timing, so a race between
+    waves (a copy landing in a slot that is still read, an LDS buffer rewritten before a barrier) shows up here as a
+    few differing rows, well inside the accuracy bars the other tests hold. 40 tokens x 6 query heads over 3000 keys:
+    two row blocks through the unrolled and steady loops; one split, or the host's choice (split partials merged)."""
+    import torch
+
+    from vllm_quantpack.attention import int4_prefill
+    rng = np.random.default_rng(260 + splits + (2 if fmt == "int8" else 0))
+    n, T, bs = 3000, 40, 16
+    nb = -(-n // bs)
+    kv, _ = random_cache(rng, nb, NKV, bs, HS, fmt)
+    _, (kc, vc, ks, vs) = torch_cache(kv, HS, fmt, device)
+    q = bf16_tensor(O.f32_to_bf16_bits(rng.standard_normal((T, NQ, HS)).astype(np.float32)), device)
+    kw = dict(cu_seqlens_q=i32([0, T], device), seqused_k=i32([n], device),
+              block_table=i32(rng.permutation(nb).astype(np.int32)[None], device), max_seqlen_q=T,
+              softmax_scale=HS ** -0.5, num_splits=splits)
+    outs = []
+    for _ in range(5):
+        out = torch.full_like(q, float("nan"))
+        int4_prefill.prefill_attention(q, kc, vc, ks, vs, out, **kw)
+        torch.cuda.synchronize()
+        outs.append(to_f32(out))
+    assert np.isfinite(outs[0]).all()
+    for k in range(1, 5):
+        diff = np.argwhere(outs[k] != outs[0])
+        assert not len(diff), (k, len(diff), sorted({(int(t), int(h)) for t, h, _ in diff})[:8])
+
+
 @pytest.mark.parametrize("fmt,n", [("int4", 330), ("int4", 1009), ("int8", 1000), ("int8", 721)])
 def test_prefill_table_row_exactly_as_long_as_the_context(device, fmt, n):
     """One sequence whose block table holds exactly ceil(n / 16) entries and whose last tile has 1..16 keys: the

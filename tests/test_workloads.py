@@ -61,6 +61,20 @@ def _prefill(w, device):
     return to_f32(out), d
 
 
+def _prefill_again(w, d):
+    """The chunked prefill once more over the cache _prefill stored into; out fp32 numpy [T, NQ, HS]."""
+    import torch
+
+    from vllm_quantpack.attention import int4_prefill
+    out = torch.empty_like(d["q"])
+    int4_prefill.prefill_attention(d["q"], d["k_cache"], d["v_cache"], d["k_scale_cache"], d["v_scale_cache"], out,
+                                   cu_seqlens_q=d["cu_seqlens_q"], seqused_k=d["seqused_k"],
+                                   block_table=d["block_table"], max_seqlen_q=w.max_query_len,
+                                   softmax_scale=w.softmax_scale)
+    torch.cuda.synchronize()
+    return to_f32(out)
+
+
 def _oracle_decode(w):
     """fp64 closed form and the reference kernel's emulation, sequence by sequence."""
     views = _views(w)
@@ -186,6 +200,8 @@ def test_full_size_prefill_workload_matches_fp64(device, name):
     ref = _full_reference(w, d)
     assert np.isfinite(out).all()
     assert O.relerr(out, ref) < 5e-3
+    # the same call again gives the same bits (a copy or barrier race shows up here as a few differing rows)
+    assert np.array_equal(_prefill_again(w, d), out)
 
 
 def test_gpu_dequant_restatement_matches_the_oracle():
