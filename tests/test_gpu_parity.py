@@ -682,25 +682,28 @@ def test_prefill_loop_boundaries(device, fmt, bs, splits):
         at += 20
 
 
-@pytest.mark.parametrize("fmt", ["int4", "int8"])
 @pytest.mark.parametrize("splits", [1, 0])
-def test_prefill_repeats_bit_for_bit(device, fmt, splits):
+@pytest.mark.parametrize("hs,nq,nkv,fmt", [(256, 24, 4, "int4"), (256, 24, 4, "int8"), (128, 64, 8, "int4"),
+                                           (128, 64, 8, "int8"), (512, 16, 2, "int4"), (512, 16, 2, "int8")])
+def test_prefill_repeats_bit_for_bit(device, fmt, splits, hs, nq, nkv):
     """The same call five times gives the same bits. Nothing in the kernels depends on timing, so a race between
-    waves (a copy landing in a slot that is still read, an LDS buffer rewritten before a barrier) shows up here as a
-    few differing rows, well inside the accuracy bars the other tests hold. 40 tokens x 6 query heads over 3000 keys:
-    two row blocks through the unrolled and steady loops; one split, or the host's choice (split partials merged)."""
+    waves (a copy landing in a slot that is still read, an LDS buffer rewritten before a barrier) or a work split that
+    follows the waves' timing shows up here as differing rows, well inside the accuracy bars the other tests hold.
+    40 tokens over 3000 keys: at head 256 (6 query heads per KV head) two row blocks of the tile kernel through its
+    unrolled and steady loops; head 128 with 8 per KV head and head 512 on the wide kernel; head 512 with int8 keys as
+    query slices on the decode kernel; one split, or the host's choice (split partials merged)."""
     import torch
 
     from vllm_quantpack.attention import int4_prefill
-    rng = np.random.default_rng(260 + splits + (2 if fmt == "int8" else 0))
+    rng = np.random.default_rng(260 + splits + (2 if fmt == "int8" else 0) + hs)
     n, T, bs = 3000, 40, 16
     nb = -(-n // bs)
-    kv, _ = random_cache(rng, nb, NKV, bs, HS, fmt)
-    _, (kc, vc, ks, vs) = torch_cache(kv, HS, fmt, device)
-    q = bf16_tensor(O.f32_to_bf16_bits(rng.standard_normal((T, NQ, HS)).astype(np.float32)), device)
+    kv, _ = random_cache(rng, nb, nkv, bs, hs, fmt)
+    _, (kc, vc, ks, vs) = torch_cache(kv, hs, fmt, device)
+    q = bf16_tensor(O.f32_to_bf16_bits(rng.standard_normal((T, nq, hs)).astype(np.float32)), device)
     kw = dict(cu_seqlens_q=i32([0, T], device), seqused_k=i32([n], device),
               block_table=i32(rng.permutation(nb).astype(np.int32)[None], device), max_seqlen_q=T,
-              softmax_scale=HS ** -0.5, num_splits=splits)
+              softmax_scale=hs ** -0.5, num_splits=splits)
     outs = []
     for _ in range(5):
         out = torch.full_like(q, float("nan"))

@@ -10,11 +10,11 @@
 // MI355X design (one workgroup of W waves per (segment, KV head, sequence)):
 //   * Every query row of the KV head's GQA group (T tokens x G heads, up to 32 rows) sits in one workgroup, so the
 //     segment's cache bytes are read from HBM once per step.
-//   * Each wave streams 32-key chunks into wave-private LDS stages: its first ones statically (chunk w, w + W, ...),
-//     the rest from a workgroup counter as stages free up. For the standard HND cache (each (block, KV head) page
-//     span of 16 cells contiguous) the span bytes go straight from HBM to LDS with global_load_lds_dwordx4 (no VGPR
-//     staging), in one or two stages per wave, waits placed by hand; any other strided layout goes through VGPR
-//     buffer loads into padded LDS rows.
+//   * Each wave streams 32-key chunks into wave-private LDS stages, chunks w, w + W, w + 2 W, ... in key order (a
+//     fixed assignment, so the fp32 sums run in the same order at every call and results repeat bit for bit). For
+//     the standard HND cache (each (block, KV head) page span of 16 cells contiguous) the span bytes go straight
+//     from HBM to LDS with global_load_lds_dwordx4 (no VGPR staging), in one or two stages per wave, waits placed by
+//     hand; any other strided layout goes through VGPR buffer loads into padded LDS rows.
 //   * 8 waves (two per SIMD) for one row tile up to head 256; 4 waves for two row tiles (their O^T accumulators in
 //     AGPRs through inline-assembly MFMAs, the query operands in VGPRs) and for head 512, where more than 16
 //     rows run as workgroups of whole tokens.
@@ -950,11 +950,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
   const int seq = d.seq, q0 = d.q0, row0 = d.row0, T = d.T, n = d.n, kstart = d.kstart, kend = d.kend;
   const int col = lane & 15, g = lane >> 4;
 
-  // Chunks are handed out in key order: the first kStages of every wave statically (chunk w + s * WAVES), the rest
-  // from a workgroup counter whenever a stage frees up. Waves whose first copies got out earlier take more of the
-  // segment, so all waves of the workgroup finish together.
-  __shared__ int next_chunk;
-  if (threadIdx.x == 0) next_chunk = kStages * WAVES;
+  // Wave w takes chunks w, w + WAVES, w + 2 WAVES, ..., alternating its stages. A workgroup counter that handed each
+  // freed stage the next unclaimed chunk balanced the waves slightly better (0-1.3 % faster), but the chunks a wave
+  // summed then depended on timing, and so did the last bits of the output.
   const bool shared_rot = p.qsigns != nullptr;
   if (shared_rot) rotate_rows_shared<HS, NCT, WAVES>(qrot, p, q0, T, h, G, w, lane);
   __syncthreads();
@@ -1000,9 +998,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
     constexpr bool kEarlyK = HS <= 256;
     if constexpr (!kEarlyK) chunk_qk<HS, KFMT, NCT, Sh::kCell>(st, cr, stage, col, g);
     chunk_load<HS, KFMT, NCT, Sh::kCell, Sh::kCell, kEarlyK>(cr, stage, stage + Sh::kKeyBytes + 4, col, g);
-    int nc = 0;
-    if (lane == 0) nc = atomicAdd(&next_chunk, 1);
-    nc = uniform(nc);
+    const int nc = c + kStages * WAVES;  // this stage's next chunk
     if (nc < nchunks) {
       // the stage's K and V codes are in registers now: refill it before the QK, softmax and PV run
       wait_lgkm0();  // every read of this stage has returned before the DMA may overwrite it
