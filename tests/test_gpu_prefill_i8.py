@@ -85,6 +85,31 @@ def test_prefill_i8_scores_far_above_the_first_tile(device):
     assert O.relerr(out, ref) < 5e-3, O.relerr(out, ref)
 
 
+def test_prefill_i8_repeats_bit_for_bit(device):
+    """Five identical calls (key splits merged) give the same bits: the kernel's work split does not follow timing."""
+    import torch
+
+    from vllm_quantpack.attention import int4_prefill
+    rng = np.random.default_rng(735)
+    hs, nq, nkv, bs, n, T = 256, 24, 4, 16, 3000, 40
+    nb = -(-n // bs)
+    kv, _ = random_cache(rng, nb, nkv, bs, hs, "int4")
+    _, (kc, vc, ks, vs) = torch_cache(kv, hs, "int4", device)
+    q = bf16_tensor(O.f32_to_bf16_bits(rng.standard_normal((T, nq, hs)).astype(np.float32)), device)
+    kw = dict(cu_seqlens_q=i32([0, T], device), seqused_k=i32([n], device),
+              block_table=i32(rng.permutation(nb).astype(np.int32)[None], device), max_seqlen_q=T,
+              softmax_scale=hs ** -0.5, num_splits=3)
+    outs = []
+    for _ in range(5):
+        out = torch.full_like(q, float("nan"))
+        int4_prefill.prefill_attention_i8(q, kc, vc, ks, vs, out, **kw)
+        torch.cuda.synchronize()
+        outs.append(to_f32(out))
+    assert np.isfinite(outs[0]).all()
+    for k in range(1, 5):
+        assert np.array_equal(outs[k], outs[0]), (k, int((outs[k] != outs[0]).sum()))
+
+
 def test_prefill_sequence_i8_contract(device):
     """The reference's call (int4_prefill.py:176): one chunk's rotated queries, the nibble and scale views, a block
     row and n; the output in the queries' dtype, against the emulation."""
