@@ -175,6 +175,25 @@ def test_random_blocks_respect_every_dependence():
         order = ms.schedule(insts)
         assert sorted(x.text for x in order) == sorted(block)
         assert _respects(order, insts)
+        # every barrier keeps the same instructions on each side
+        pos = {id(x): k for k, x in enumerate(order)}
+        for b, x in enumerate(insts):
+            if x.op == "S_BARRIER":
+                assert all(pos[id(y)] < pos[id(x)] for y in insts[:b])
+                assert all(pos[id(y)] > pos[id(x)] for y in insts[b + 1:-1])
+
+
+def test_barrier_is_a_full_fence():
+    """Register-only instructions (the scalar adds forming copy addresses, VALU work, MFMAs) stay on their side of a
+    barrier in the middle of a block, although no register or memory dependence ties them to it."""
+    before = ["renamable $sgpr13 = S_ADD_I32 renamable $sgpr18, killed renamable $sgpr13, implicit-def dead $scc",
+              fma(10, 11, 12, 13), mfma(20, 30, 40)]
+    after = [mfma(24, 30, 44), fma(14, 15, 16, 17),
+             "renamable $sgpr12 = S_ADD_I32 renamable $sgpr18, killed renamable $sgpr12, implicit-def dead $scc"]
+    block = before + ["S_BARRIER"] + after + ["S_BRANCH %bb.3"]
+    order = [x.text for x in ms.schedule([ms.Inst(t) for t in block])]
+    bar = order.index("S_BARRIER")
+    assert all(order.index(t) < bar for t in before) and all(order.index(t) > bar for t in after)
 
 
 MIR = """--- |

@@ -24,6 +24,10 @@ remaining path whose operands are ready fills the issue slots. Dependences:
     its order relative to all the others of that kind;
   * inline assembly reads EXEC (its vector instructions run under it, though the statement does not list it), so
     it never moves across an EXEC write such as a lane-masked region's s_and_saveexec;
+  * a barrier (s_barrier) is a full fence: every instruction before it stays before it and every one after it stays
+    after it, register-only ones included. A variant that let the scalar add forming an LDS-DMA copy's M0 value move
+    from before a barrier to just after it gave results that differed from call to call (the cause was not found);
+    with the fence the prefill kernels measure the same;
   * inline-assembly MFMAs (invisible to LLVM's hazard recognizer): one that carries trailing wait states stays after
     every earlier inline MFMA of its block, and no later one moves above it, so the wait states still follow the
     last of them;
@@ -186,7 +190,14 @@ def dependences(insts):
         if j is not None and j != i:
             preds[i][j] = max(preds[i].get(j, 0), lat)
 
+    last_barrier = None
     for i, ins in enumerate(insts):
+        if ins.op.startswith("S_BARRIER"):  # a full fence (module docstring)
+            for j in range(i):
+                edge(i, j, 1)
+            last_barrier = i
+        else:
+            edge(i, last_barrier, 1)
         for u in ins.uses:
             if u in last_def:
                 edge(i, last_def[u], insts[last_def[u]].lat)
