@@ -2,7 +2,8 @@
 
 prefill_kernel (csrc/qp_prefill.hip) and prefill_wide_kernel (csrc/qp_prefill_wide.hip) read the table pair of tile
 t + 5 one iteration ahead of its copies, through a pointer that steps two entries per tile; the tile kernel's
-six-phase unrolled loop of int4 keys reads the 12 entries of tiles it + 5 .. it + 10 at once, in its first iteration.
+six-phase unrolled loop of int4 keys reads the 12 entries of tiles it + 5 .. it + 10 at once, in its first iteration,
+and its rolled steady loop of int8 keys runs in pairs whose first iteration reads the 4 entries of tiles it + 5, it + 6.
 Their steady iterations (that unrolled loop, the tile kernel's rolled steady loop of int8 keys, the wide kernel's
 steady loop) take a pair's second entry without checking the split's end, which is only valid when that tile is
 followed by another one. This walk restates each kernel's loop structure (prologue and loops, with the `kPfSteadyLead` bound read
@@ -34,6 +35,8 @@ def steady_lead() -> int:
     assert "it + 5 + kPfSteadyLead <= ntiles" in src
     # the unrolled loop's group read, as walked below
     assert "for (int k = 0; k < 12; ++k) tb[k] = tnext[k];" in src and "tnext += 12;" in src
+    assert "for (int k = 0; k < 4; ++k) tb[k] = tnext[k];" in src and "tnext += 4;" in src
+    assert "it + 1 < nplain && it + 1 + kPfSteadyLead <= ntiles; it += 2" in src
     assert "it + kPfSteadyLead <= ntiles" in (CSRC / "qp_prefill_wide.hip").read_text()
     return int(m.group(1))
 
@@ -93,6 +96,14 @@ def walk(n, qlen, t_first, t_last, split, splits, int4, lead, wide=False):
                 state["next_tile"] += 6
                 it += 6
         else:
+            while it + 1 < nplain and it + 1 + lead <= ntiles:
+                # the pair's first iteration reads tnext .. tnext + 3: the pairs of tiles it + 5, it + 6
+                assert state["next_tile"] == it + 5
+                tn = state["tnext"]
+                reads.extend((it + 5 + k // 2, tn + k) for k in range(4))
+                state["tnext"] += 4
+                state["next_tile"] += 2
+                it += 2
             while it < nplain and it + lead <= ntiles:
                 iteration(it, True)
                 it += 1
