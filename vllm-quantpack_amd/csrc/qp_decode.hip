@@ -883,10 +883,14 @@ struct SpanShape {
 
 template <class Sh>
 __device__ __forceinline__ void issue_span_dma(const DecodeParams &p, const int32_t *trow, int k0, int kend, int h,
-                                               int lane, uint8_t *stage) {
+                                               int lane, uint8_t *stage, int given0 = -1, int given1 = -1) {
   // a half at or past kend re-reads half 0 (valid memory) so that every chunk issues the same count of loads
   int bidx[2], slot[2], bid[2];
-  if (p.block_size == 16) {  // chunks start at multiples of 32 keys: each half is a whole block
+  if (given0 >= 0) {  // 16-token blocks, block ids already read by the caller
+    bid[0] = given0;
+    bid[1] = given1;
+    slot[0] = slot[1] = 0;
+  } else if (p.block_size == 16) {  // chunks start at multiples of 32 keys: each half is a whole block
     bidx[0] = uniform(k0 >> 4);
     bidx[1] = uniform(k0 + 16 < kend ? bidx[0] + 1 : bidx[0]);
     slot[0] = slot[1] = 0;
@@ -898,7 +902,7 @@ __device__ __forceinline__ void issue_span_dma(const DecodeParams &p, const int3
       slot[hc] = pos - bidx[hc] * p.block_size;
     }
   }
-  table_pair(trow, bidx[0], bidx[1], bid[0], bid[1]);
+  if (given0 < 0) table_pair(trow, bidx[0], bidx[1], bid[0], bid[1]);
   // each half is one contiguous run: a scalar base and the lanes' fixed offsets (nontemporal: the stream is read once)
   const uint32_t lds = lds_addr(stage);
 #pragma unroll
@@ -964,6 +968,18 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
   constexpr int kWordK = Sh::kKeyBytes, kWordV = Sh::kCell - 4;
 
   // The query rows load first: their wait is on the vm counter, which would otherwise also wait for the copies.
+  // With 16-token blocks and at most 32 chunks per wave, the block ids of the wave's chunks come in one vector load
+  // before the copies start: lane 2 k + hc holds half hc of the wave's k-th chunk (the block after the chunk's first,
+  // or the first again when the second half starts at or past kend, as the copies read it).
+  const bool tab_lanes = p.block_size == 16 && nchunks <= 32 * WAVES;
+  int tabv = 0;
+  if (tab_lanes) {
+    const int c = w + WAVES * (lane >> 1);
+    if (c < nchunks) {
+      const int k0 = kstart + c * kChunk;
+      tabv = trow[(k0 >> 4) + ((lane & 1) && k0 + 16 < kend ? 1 : 0)];
+    }
+  }
   WaveState<HS, KFMT, NCT> st;
   init_state(st, p, q0, T, n, h, G, col, g, shared_rot ? qrot : nullptr);
   if constexpr (!kQrotOwn) {
@@ -973,7 +989,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
 #pragma unroll
   for (int s0 = 0; s0 < kStages; ++s0) {
     cid[s0] = w + s0 * WAVES < nchunks ? w + s0 * WAVES : -1;
-    if (cid[s0] >= 0) issue_span_dma<Sh>(p, trow, kstart + cid[s0] * kChunk, kend, h, lane, wl + s0 * 2 * Sh::kHalf);
+    if (cid[s0] >= 0) {
+      const int kk = s0;  // the wave's s0-th chunk
+      issue_span_dma<Sh>(p, trow, kstart + cid[s0] * kChunk, kend, h, lane, wl + s0 * 2 * Sh::kHalf,
+                         tab_lanes ? __builtin_amdgcn_readlane(tabv, 2 * kk) : -1,
+                         tab_lanes ? __builtin_amdgcn_readlane(tabv, 2 * kk + 1) : -1);
+    }
   }
 
   // one chunk through stage si; false when the stage is empty (then so is every later one)
@@ -1003,7 +1024,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_span_kernel(const DecodePar
       // the stage's K and V codes are in registers now: refill it before the QK, softmax and PV run
       wait_lgkm0();  // every read of this stage has returned before the DMA may overwrite it
       wave_sync();
-      issue_span_dma<Sh>(p, trow, kstart + nc * kChunk, kend, h, lane, stage);
+      const int kk = (nc - w) / WAVES;  // the wave's kk-th chunk
+      issue_span_dma<Sh>(p, trow, kstart + nc * kChunk, kend, h, lane, stage,
+                         tab_lanes ? __builtin_amdgcn_readlane(tabv, 2 * kk) : -1,
+                         tab_lanes ? __builtin_amdgcn_readlane(tabv, 2 * kk + 1) : -1);
       cid[si] = nc;
     } else {
       cid[si] = -1;
