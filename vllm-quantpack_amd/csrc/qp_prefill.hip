@@ -14,8 +14,8 @@
 //
 // MI355X design. A workgroup of 4 waves (one per SIMD) owns (row block, KV head, key split). A row block is 64 NT
 // consecutive (token, query head) pairs of one sequence in token-major order, so any GQA width fills it, cut into
-// 4 * NT row tiles of 16 rows; wave w owns tiles w, w + 4, w + 8, so each K / V operand read from LDS feeds NT MFMAs
-// and every K/V tile is dequantised once for all the block's rows.
+// 4 * NT row tiles of 16 rows; wave w owns tiles w, w + 4, ... (NT of them), so each K / V operand read from LDS
+// feeds NT MFMAs and every K/V tile is dequantised once for all the block's rows.
 // Per 32-key tile, with one barrier:
 //   * the tile's two 16-key page runs come HBM -> LDS (global_load_lds_dwordx4) into one of three packed slots,
 //     issued four tiles ahead of the tile whose PV runs, from one scalar base per page run and fixed lane offsets;
@@ -41,6 +41,7 @@
 // (acc, m, l) in the split-KV layout and qp_merge_segments combines them (with the inverse rotation when asked).
 #include "qp_prefill.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace qp {
@@ -253,7 +254,7 @@ struct PfStager {
 // destination within 18 wait states and fails if it finds one.
 template <int NT>
 __device__ __forceinline__ void pv_step(f32x4_t (&acc)[NT][17], int b, bf16x8_t vop, const u32x4_t (&pop)[NT]) {
-  static_assert(NT >= 1 && NT <= 3, "row tiles");
+  static_assert(NT >= 1 && NT <= 4, "row tiles");
   // (the accumulator array is sized for head 256; head 128 uses tiles 0..8)
   // One statement per MFMA, so that VALU work can be placed between them.
 #pragma unroll
@@ -279,7 +280,8 @@ template <int NT>
 __device__ __forceinline__ void p_ready(u32x4_t (&pop)[NT]) {
   if constexpr (NT == 1) asm volatile("s_nop 1" : "+v"(pop[0]));
   else if constexpr (NT == 2) asm volatile("s_nop 1" : "+v"(pop[0]), "+v"(pop[1]));
-  else asm volatile("s_nop 1" : "+v"(pop[0]), "+v"(pop[1]), "+v"(pop[2]));
+  else if constexpr (NT == 3) asm volatile("s_nop 1" : "+v"(pop[0]), "+v"(pop[1]), "+v"(pop[2]));
+  else asm volatile("s_nop 1" : "+v"(pop[0]), "+v"(pop[1]), "+v"(pop[2]), "+v"(pop[3]));
 }
 
 // one QK step (32 channels of one 16-key sub-tile) for every row tile of the wave
@@ -889,8 +891,11 @@ using namespace qp;
 namespace {
 
 // Row tiles per wave: 3 (192 (token, query head) rows per workgroup), or fewer when the longest chunk holds fewer rows.
-int prefill_nt(int G, int max_query_len) {
+// At head 128 a chunk of more than 192 rows takes 4 (256 rows; 148 AGPRs and 256 VGPRs, no spill): 2.86-2.89 against
+// 3.00-3.04 ms on a 1024-token chunk of 32 q / 8 KV heads over 131072 keys, with the splits below.
+int prefill_nt(int G, int max_query_len, int hs) {
   const int64_t rows = (int64_t)(max_query_len > 0 ? max_query_len : 1) * G;
+  if (hs == 128 && rows > 192) return 4;
   return rows > 128 ? 3 : rows > 64 ? 2 : 1;
 }
 
@@ -899,7 +904,12 @@ int prefill_splits(const qp_paged_cache *cache, const qp_prefill_args *a, int nt
   if (a->num_splits > 0) return a->num_splits;
   const int64_t rows = (int64_t)kPfWaves * 16 * nt;
   const int64_t blocks = ((int64_t)a->num_tokens * (a->num_q_heads / cache->num_kv_heads) + rows - 1) / rows;
-  return balanced_splits(blocks * cache->num_kv_heads, a, 1);
+  // four row tiles: splits of at most about 300 tiles (9600 keys). With the 2 splits the rounds alone give, each
+  // workgroup streamed 2064 tiles, 8.9 MB of keys and values that its row-block neighbours no longer shared through
+  // L2, and the chunk above took 4.81 ms; 8 splits 3.06 ms, 14 splits 2.87 ms. (Three row tiles gain nothing from
+  // more splits.)
+  const int min_s = nt == 4 ? (int)std::min<int64_t>(64, std::max<int64_t>(1, ((int64_t)a->max_seqlen_k + 9599) / 9600)) : 1;
+  return balanced_splits(blocks * cache->num_kv_heads, a, min_s);
 }
 
 int64_t partial_bytes(const qp_paged_cache *cache, const qp_prefill_args *a, int splits) {
@@ -919,7 +929,12 @@ template <int HS, int KFMT>
 void dispatch_nt(const PrefillParams &p, int nt, dim3 grid, bool span, hipStream_t s) {
   if (nt == 1) launch_prefill<HS, KFMT, 1>(p, grid, span, s);
   else if (nt == 2) launch_prefill<HS, KFMT, 2>(p, grid, span, s);
-  else launch_prefill<HS, KFMT, 3>(p, grid, span, s);
+  else if constexpr (HS == 128) {
+    if (nt == 4) launch_prefill<HS, KFMT, 4>(p, grid, span, s);
+    else launch_prefill<HS, KFMT, 3>(p, grid, span, s);
+  } else {
+    launch_prefill<HS, KFMT, 3>(p, grid, span, s);
+  }
 }
 
 // Which kernel serves a prefill (measured over 1024-token chunks at contexts of 32768 and 131072 keys):
@@ -960,7 +975,7 @@ extern "C" int64_t qp_prefill_workspace_size(const qp_paged_cache *cache, const 
   if (path == PrefillPath::kSlices) return slice_prefill_workspace(cache, a);
   if (path == PrefillPath::kWide) return partial_bytes(cache, a, wide_splits(cache, a));
   return partial_bytes(cache, a, prefill_splits(cache, a, prefill_nt(a->num_q_heads / cache->num_kv_heads,
-                                                                    a->max_query_len)));
+                                                                    a->max_query_len, cache->head_size)));
 }
 
 namespace qp {
@@ -1077,7 +1092,7 @@ int prefill_run(const qp_paged_cache *cache, const qp_prefill_args *a, const int
   const PrefillPath path = prefill_path(cache, a);
   if (path == PrefillPath::kSlices) return slice_prefill(cache, a, skip_seq, s);
   const bool wide = path == PrefillPath::kWide;
-  const int nt = wide ? 0 : prefill_nt(G, a->max_query_len);
+  const int nt = wide ? 0 : prefill_nt(G, a->max_query_len, hs);
   int splits = wide ? wide_splits(cache, a) : prefill_splits(cache, a, nt);
   if (splits > 1 && (!a->workspace || a->workspace_bytes < partial_bytes(cache, a, splits))) {
     QP_REQUIRE(a->num_splits == 0, "qp_prefill: workspace too small for the requested splits");
